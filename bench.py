@@ -1,0 +1,250 @@
+"""Benchmark: routed GQA prefill on one MI355X.
+
+Metric: routed-attention TFLOP/s and ms per prefill at
+S=16k Hq32/Hkv8, plus the fraction of bf16 MFMA peak.
+
+Workload (the config the metric is quoted on): B=1, S=16384, Hq=32, Hkv=8,
+d=128, window 1024, Bernoulli(p_full=0.25) routing, bf16 N(0,1) inputs drawn
+on the CPU with a fixed seed and moved to HBM before timing.
+
+One step = one routed prefill through the public API, exactly as a caller
+runs it: build_switch_query_indices(mask) + switch_gqa_prefill_forward(...)
+(compaction, index validation with its device-to-host flag read, and the
+attention launch).  value = routed FLOPs / step time, where routed FLOPs are
+counted exactly from the mask (4*d*Hq per legal query/key pair).
+
+The JSON line also carries:
+* roofline: the attention kernel alone, timed with HIP events on the stream it
+  runs on, against the 2516.6 TFLOP/s dense bf16 MFMA peak;
+* cpu_baseline: the fp32 PyTorch oracle (a restatement of the reference's
+  semantics -- the reference has no CPU path) on a bounded random row sample
+  of the same workload, on this host's cores;
+* comparators: the same kernel on all-full routing (dense causal), and
+  torch SDPA causal (flash backend) on the same shape.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (AMD public spec)
+PEAK_HBM_GBS = 8000.0
+METRIC = "routed-attn TFLOP/s + ms/prefill at S=16k Hq32/Hkv8; % of bf16 MFMA peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--p-full", type=float, default=0.25)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="budget for the CPU baseline sample (0 disables it)")
+    ap.add_argument("--no-sdpa", action="store_true", help="skip the torch SDPA comparator")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only loop the attention kernel (for rocprofv3 runs)")
+    return ap.parse_args()
+
+
+def time_launches(fn, iters, warmup=3):
+    """Average ms per call of fn() between two events on torch's current stream."""
+    for _ in range(warmup):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                          "(sharding across GPUs is described in DESIGN.md, not implemented)"}))
+        sys.exit(2)
+
+    from switchattentionkernels_amd import (build_switch_query_indices, routed_flops,
+                                            switch_gqa_prefill_forward, workloads)
+    from switchattentionkernels_amd import _lib
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = workloads.build("s16k", seed=args.seed, p_full=args.p_full)
+    desc = wl["workload"]
+    B, S, HQ, HKV, D, W = desc.batch, desc.seq_len, desc.heads_q, desc.heads_kv, 128, desc.window
+    q, k, v = wl["q"].to(dev), wl["k"].to(dev), wl["v"].to(dev)
+    mask = wl["mask"].to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        full, local = build_switch_query_indices(mask)
+        return switch_gqa_prefill_forward(q, k, v, full, local, window_size=W)
+
+    full, local = build_switch_query_indices(mask)
+    flops = routed_flops(full, local, batch=B, seq_q=S, seq_kv=S, heads_q=HQ, head_dim=D,
+                         window=W)
+    dense_flops = 4 * D * HQ * B * S * (S + 1) // 2
+    L = _lib.lib()
+    scale = D ** -0.5 * 1.4426950408889634
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def attn(fi, li):
+        st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), fi.data_ptr(),
+                                  fi.numel(), li.data_ptr(), li.numel(), None, None, None,
+                                  out.data_ptr(), lse.data_ptr(), B, S, S, HQ, HKV, D, W, scale,
+                                  stream)
+        if st != 0:
+            raise RuntimeError(L.swattn_last_error().decode())
+
+    if args.kernel_only:
+        for _ in range(args.warmup + args.steps):
+            attn(full, local)
+        torch.cuda.synchronize()
+        print(json.dumps({"kernel_only": True, "launches": args.warmup + args.steps}))
+        return
+
+    # ---- timed region: K full steps -------------------------------------------
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    print(f"[bench] {args.steps} steps, {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # ---- attention kernel alone (roofline) -------------------------------------
+    attn_ms = time_launches(lambda: attn(full, local), max(args.steps, 10))
+    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
+    ones = torch.ones_like(mask)
+    f_all, l_all = build_switch_query_indices(ones)
+    dense_ms = time_launches(lambda: attn(f_all, l_all), max(args.steps // 2, 5))
+    ws_bytes = int(L.swattn_compact_workspace_bytes(S * B))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    idx = torch.empty(S * B, dtype=torch.int32, device=dev)
+    cnt = torch.empty(2, dtype=torch.int32, device=dev)
+    compact_ms = time_launches(lambda: L.swattn_compact(mask.data_ptr(), S * B, idx.data_ptr(),
+                                                        cnt.data_ptr(), ws.data_ptr(), ws_bytes,
+                                                        stream), 50)
+    compact_bytes = S * B + 4 * S * B + 8
+    print(f"[bench] attention kernel {attn_ms:.3f} ms ({attn_tflops:.1f} TFLOP/s); dense causal "
+          f"{dense_ms:.3f} ms; compaction {compact_ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+
+    # ---- SDPA comparator (flash backend, GQA expanded) -------------------------
+    sdpa_ms = None
+    if not args.no_sdpa:
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            g = HQ // HKV
+            qt = q.permute(0, 2, 1, 3).contiguous()
+            kt = k.repeat_interleave(g, dim=2).permute(0, 2, 1, 3).contiguous()
+            vt = v.repeat_interleave(g, dim=2).permute(0, 2, 1, 3).contiguous()
+            with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+                sdpa_ms = time_launches(lambda: torch.nn.functional.scaled_dot_product_attention(
+                    qt, kt, vt, is_causal=True), 5, warmup=2)
+            del qt, kt, vt
+        except Exception as exc:  # comparator only
+            print(f"[bench] SDPA comparator unavailable: {exc}", file=sys.stderr, flush=True)
+
+    # ---- traffic (committed rocprofv3 --pmc result, if any) ---------------------
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "fwd_s16k_p25_traffic.txt")
+    if os.path.exists(tpath):
+        for line in open(tpath):
+            if line.startswith("traffic_bytes_per_launch"):
+                traffic = int(float(line.split("=")[1]))
+
+    # ---- CPU baseline: the oracle on a bounded row sample -------------------------
+    cpu = None
+    if args.cpu_seconds > 0:
+        import numpy as np
+        import oracle
+        from oracle import routing as R
+        f_np, l_np = R.compact(wl["mask"].numpy())
+        chunk = 256
+        blocks = torch.randperm((B * S) // chunk,
+                                generator=torch.Generator().manual_seed(1)).tolist()
+        done, t_cpu = [], 0.0
+        with torch.inference_mode():
+            oracle.routed_attention(wl["q"], wl["k"], wl["v"], f_np, l_np, window_size=W,
+                                    rows=np.arange(chunk))   # warm-up
+            for blk in blocks:
+                if t_cpu >= args.cpu_seconds:
+                    break
+                r = np.arange(blk * chunk, (blk + 1) * chunk)
+                t1 = time.perf_counter()
+                oracle.routed_attention(wl["q"], wl["k"], wl["v"], f_np, l_np, window_size=W,
+                                        rows=r)
+                t_cpu += time.perf_counter() - t1
+                done.append(r)
+        sample = np.concatenate(done)
+        rows_done = sample.size
+        is_full = np.zeros(B * S, dtype=bool)
+        is_full[f_np] = True
+        i = sample % S
+        pairs = np.where(is_full[sample], i + 1, np.minimum(i + 1, W)).sum()
+        cpu_flops = 4 * D * HQ * int(pairs)
+        cpu = {"value": round(cpu_flops / t_cpu / 1e12, 4), "unit": "TFLOP/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{rows_done} query rows (all {HQ} heads) in {len(done)} random "
+                         f"{chunk}-row blocks of the s16k p_full="
+                         f"{args.p_full} workload, fp32 dense-masked torch oracle, "
+                         f"{t_cpu:.1f} s; host {os.cpu_count()} cpus, affinity "
+                         f"{len(os.sched_getaffinity(0))}",
+               "ms_per_prefill_extrapolated": round(t_cpu * 1e3 * B * S / rows_done, 1)}
+
+    achieved = attn_tflops
+    res = {
+        "metric": METRIC,
+        "value": round(flops / (ms_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded bf16 N(0,1) Q/K/V, Bernoulli route mask)",
+        "config": {"workload": f"s16k: B{B} S{S} Hq{HQ}/Hkv{HKV} d{D} W{W} "
+                               f"p_full={args.p_full} Bernoulli, seed {args.seed}",
+                   "batch": B, "seq_len": S, "heads_q": HQ, "heads_kv": HKV, "head_dim": D,
+                   "window": W, "p_full": args.p_full, "routed_gflop": round(flops / 1e9, 2)},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "kernel": "fwd_kernel<false> (swattn_prefill_fwd)",
+                     "kernel_ms": round(attn_ms, 4)},
+        "cpu_baseline": cpu,
+        "comparators": {
+            "dense_causal_same_kernel_ms": round(dense_ms, 4),
+            "routed_flop_fraction": round(flops / dense_flops, 4),
+            "routed_over_dense_time": round(attn_ms / dense_ms, 4),
+            "sdpa_flash_causal_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
+            "compaction_us": round(compact_ms * 1e3, 2),
+            "compaction_gbs": round(compact_bytes / (compact_ms * 1e-3) / 1e9, 1),
+        },
+    }
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,128 @@
+/*
+ * swattn.h -- C ABI of libswattn.so, the MI355X (gfx950) Switch Attention
+ * prefill library.
+ *
+ * Every entry point takes device pointers, plain sizes and a hipStream_t
+ * (passed as void*; NULL = the legacy default stream), enqueues its kernels on
+ * that stream and returns without synchronising.  Nothing here allocates
+ * device memory: scratch space is passed in by the caller.
+ *
+ * Return value: SWATTN_OK (0) on success, a negative SWATTN_E* code for an
+ * invalid argument detected on the host, or a positive hipError_t from the
+ * launch.  swattn_last_error() gives a message for the calling thread.
+ *
+ * Reference tags: V = swiattn_gqa_prefill_varlen.py,
+ *                 F = swiattn_gqa_prefill.py  (YushengZhao/SwitchAttentionKernels)
+ */
+#ifndef SWATTN_H_
+#define SWATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SWATTN_OK 0
+#define SWATTN_EINVAL (-1)      /* bad size, null pointer or unsupported shape */
+#define SWATTN_EWORKSPACE (-2)  /* workspace smaller than required            */
+
+/* Error bits written by swattn_check_indices, in the order the reference
+ * raises them (V:384-393). */
+#define SWATTN_ERR_FULL_RANGE 1   /* V:299-300 "query index is outside [0, sequence_length)" */
+#define SWATTN_ERR_FULL_ORDER 2   /* V:301-302 "query indices must be strictly increasing"   */
+#define SWATTN_ERR_LOCAL_RANGE 4  /* V:299-300, local list                                    */
+#define SWATTN_ERR_LOCAL_ORDER 8  /* V:301-302, local list                                    */
+#define SWATTN_ERR_OVERLAP 16     /* a position in both lists (contract of V:341-342)         */
+
+/* Library version, (major << 16) | minor. */
+int swattn_version(void);
+
+/* Message for the last non-zero status returned on the calling thread. */
+const char* swattn_last_error(void);
+
+/*
+ * Router-mask compaction.  Replaces build_switch_query_indices (V:306-322),
+ * whose body is `arange(S)[mask], arange(S)[~mask]` over torch's nonzero.
+ *
+ *   mask     n bytes, nonzero = routed to full causal attention.  A [B, S]
+ *            mask is passed flattened; positions are then b*S + i.
+ *   indices  n int32 outputs: the ascending full list in [0, nf), followed by
+ *            the ascending local list in [nf, n).
+ *   counts   2 int32 outputs: {nf, n - nf}.
+ *   workspace/workspace_bytes: at least swattn_compact_workspace_bytes(n).
+ * Bit-exact with the reference: both lists are the stable compaction.
+ */
+size_t swattn_compact_workspace_bytes(int64_t n);
+int swattn_compact(const uint8_t* mask, int64_t n, int32_t* indices, int32_t* counts,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Index-list validation in one pass.  Replaces the device-side checks of
+ * _prepare_indices (V:299-302, applied to both lists) and adds the
+ * disjointness the docstring requires (V:341-342).  The count-based coverage
+ * check (V:392-393) needs no device work and stays with the caller.
+ *
+ *   full/local  ascending int32 lists (n_full / n_local entries)
+ *   seq_len     positions must lie in [0, seq_len)
+ *   flags       1 int32 output: OR of SWATTN_ERR_* bits (0 = valid).
+ * The caller reads `flags` back (one 4-byte device-to-host copy).
+ */
+int swattn_check_indices(const int32_t* full, int64_t n_full, const int32_t* local,
+                         int64_t n_local, int64_t seq_len, int32_t* flags, void* stream);
+
+/*
+ * Position metadata for packed (varlen) sequences.  Replaces
+ * build_switch_attention_metadata, imported by V:27 and called at V:353-359
+ * but not shipped with the reference; the seven outputs are the fields the
+ * wrapper validates at V:360-383 and the kernel reads at V:134-137.
+ *
+ *   cu_seqlens_q / cu_seqlens_kv  num_seqs+1 ascending int32 offsets (device)
+ *   total_q / total_kv            cu_seqlens_*[num_seqs]
+ *   outputs (int32, device):  q_positions[total_q], kv_positions[total_kv],
+ *     q_segment_ids[total_q], kv_segment_ids[total_kv], full_starts[total_q],
+ *     local_starts[total_q], causal_ends[total_q].
+ * For query i (0-based inside its segment) with KV segment [ks, ke):
+ *   full_starts = ks, local_starts = ks + max(i - window + 1, 0),
+ *   causal_ends = ks + min(i + 1, ke - ks)      (F:145-155 per segment).
+ */
+int swattn_build_metadata(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv,
+                          int32_t num_seqs, int64_t total_q, int64_t total_kv, int32_t window,
+                          int32_t* q_positions, int32_t* kv_positions, int32_t* q_segment_ids,
+                          int32_t* kv_segment_ids, int32_t* full_starts, int32_t* local_starts,
+                          int32_t* causal_ends, void* stream);
+
+/*
+ * Routed GQA prefill forward, both branches in one launch.  Replaces the two
+ * _switch_gqa_prefill_branch launches of switch_gqa_prefill_forward
+ * (V:402-445; kernel body V:103-249, fixed-length rule F:69-214).
+ *
+ *   q    bf16 [batch, seq_q, heads_q, 128]   (contiguous)
+ *   k,v  bf16 [batch, seq_kv, heads_kv, 128] (contiguous)
+ *   full_idx / local_idx  ascending flattened row positions b*seq_q + i
+ *                         (n_full + n_local rows, disjoint; pre-validated)
+ *   full_starts, local_starts, causal_ends: per flattened query row key
+ *        bounds in flattened key coordinates b*seq_kv + j; all three NULL
+ *        selects F's rule (full: [0, i], local: [max(i-window+1, 0), i],
+ *        both clipped to j < seq_kv) inside each batch row.
+ *   out  bf16 [batch, seq_q, heads_q, 128], lse fp32 [batch, seq_q, heads_q]:
+ *        rows listed in full_idx/local_idx are written; others untouched.
+ *        lse uses the log2 convention: log2(sum_j 2^(s_j*c)) with
+ *        c = scale_log2 and s_j the raw q.k products (V:236-241).
+ *   scale_log2  softmax scale already multiplied by log2(e) (V:73-76).
+ */
+int swattn_prefill_fwd(const void* q, const void* k, const void* v,
+                       const int32_t* full_idx, int64_t n_full,
+                       const int32_t* local_idx, int64_t n_local,
+                       const int32_t* full_starts, const int32_t* local_starts,
+                       const int32_t* causal_ends, void* out, float* lse,
+                       int32_t batch, int64_t seq_q, int64_t seq_kv, int32_t heads_q,
+                       int32_t heads_kv, int32_t head_dim, int32_t window, float scale_log2,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SWATTN_H_ */

@@ -1,0 +1,169 @@
+"""Floating-point side of the Switch Attention oracle.
+
+TEST INFRASTRUCTURE ONLY -- see the package docstring.  Reference file tags:
+V = swiattn_gqa_prefill_varlen.py, F = swiattn_gqa_prefill.py.
+
+Semantics restated (V:103-249):
+* each query row q, for every query head h, attends to the keys
+  ``[start(q), end(q))`` of KV head ``h // (Hq // Hkv)`` (V:124, V:186-196);
+  ``start`` is the row's full or local start depending on its route;
+* scores are ``q . k`` scaled by ``sm_scale`` (default ``D**-0.5``, V:73-76);
+* ``O = softmax(scores) @ V`` and ``LSE = logsumexp(scores) * log2(e)``
+  (log2 convention, V:236-241);
+* rows are written back to their own positions (V:243-249).
+
+The restatement is a dense masked computation in fp32 on the CPU -- no online
+softmax, no bf16 rounding of P -- so it is the exact-arithmetic target that
+the kernels are compared against within a tolerance.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from .routing import default_bounds
+
+LOG2E = 1.4426950408889634
+
+
+def row_bounds(full_idx, local_idx, full_starts, local_starts, ends):
+    """Per-row ``[start, end)`` for a routed sequence (V:134-137).
+
+    Rows in ``full_idx`` take ``full_starts``, rows in ``local_idx`` take
+    ``local_starts``; every row takes ``ends``.
+    """
+    n = np.asarray(ends).size
+    start = np.full(n, -1, dtype=np.int64)
+    fi = np.asarray(full_idx, dtype=np.int64).reshape(-1)
+    li = np.asarray(local_idx, dtype=np.int64).reshape(-1)
+    start[fi] = np.asarray(full_starts, dtype=np.int64)[fi]
+    start[li] = np.asarray(local_starts, dtype=np.int64)[li]
+    return start, np.asarray(ends, dtype=np.int64).copy()
+
+
+def _bounds_for(q, k, full_idx, local_idx, window_size, metadata):
+    batch, seq_q = int(q.shape[0]), int(q.shape[1])
+    seq_kv = int(k.shape[1])
+    if metadata is None:
+        fs, ls, en = default_bounds(batch, seq_q, seq_kv, window_size)
+    else:
+        fs = np.asarray(metadata["full_starts"], dtype=np.int64)
+        ls = np.asarray(metadata["local_starts"], dtype=np.int64)
+        en = np.asarray(metadata["causal_ends"], dtype=np.int64)
+    start, end = row_bounds(full_idx, local_idx, fs, ls, en)
+    total_kv = batch * seq_kv
+    return np.clip(start, 0, total_kv), np.clip(end, 0, total_kv)
+
+
+def routed_attention(q, k, v, full_idx, local_idx, *, window_size=1024,
+                     metadata=None, sm_scale=None, rows=None, chunk=256):
+    """Dense masked routed attention in fp32.
+
+    q: ``[B, Sq, Hq, D]``, k/v: ``[B, Skv, Hkv, D]`` (any float dtype, CPU).
+    ``full_idx``/``local_idx`` are flattened row positions ``b*Sq + i``.
+    ``metadata`` (optional) is a dict with ``full_starts``, ``local_starts``,
+    ``causal_ends`` in flattened key coordinates.  ``rows`` (optional) limits
+    the computation to a subset of flattened rows (for bounded timing samples).
+
+    Returns ``(O fp32 [B, Sq, Hq, D], LSE fp32 [B, Sq, Hq])``; rows outside
+    ``rows`` are left NaN.
+    """
+    batch, seq_q, hq, d = (int(x) for x in q.shape)
+    hkv = int(k.shape[2])
+    g = hq // hkv
+    scale = (1.0 / d) ** 0.5 if sm_scale is None else float(sm_scale)
+    start, end = _bounds_for(q, k, full_idx, local_idx, window_size, metadata)
+    qf = q.reshape(batch * seq_q, hq, d).float()
+    kf = k.reshape(-1, hkv, d).float()
+    vf = v.reshape(-1, hkv, d).float()
+    out = torch.full((batch * seq_q, hq, d), float("nan"), dtype=torch.float32)
+    lse = torch.full((batch * seq_q, hq), float("nan"), dtype=torch.float32)
+    all_rows = np.arange(batch * seq_q) if rows is None else np.asarray(rows)
+    for c0 in range(0, all_rows.size, chunk):
+        r = all_rows[c0:c0 + chunk]
+        ks, ke = int(start[r].min()), int(end[r].max())
+        ke = max(ke, ks)
+        span = torch.arange(ks, ke)
+        legal = (span[None, :] >= torch.from_numpy(start[r])[:, None]) & \
+                (span[None, :] < torch.from_numpy(end[r])[:, None])          # [R, L]
+        qr = qf[torch.from_numpy(r)].reshape(len(r), hkv, g, d)             # [R, Hkv, G, D]
+        qr = qr.permute(1, 0, 2, 3).reshape(hkv, len(r) * g, d)             # [Hkv, R*G, D]
+        kt = kf[ks:ke].permute(1, 2, 0).contiguous()                        # [Hkv, D, L]
+        s = torch.bmm(qr, kt).reshape(hkv, len(r), g, ke - ks) * scale      # [Hkv, R, G, L]
+        s = s.masked_fill(~legal[None, :, None, :], float("-inf"))
+        lse_nat = torch.logsumexp(s, dim=-1)                                # [Hkv, R, G]
+        p = torch.exp(s - lse_nat[..., None])
+        o = torch.bmm(p.reshape(hkv, len(r) * g, ke - ks),
+                      vf[ks:ke].permute(1, 0, 2).contiguous())              # [Hkv, R*G, D]
+        o = o.reshape(hkv, len(r), g, d).permute(1, 0, 2, 3).reshape(len(r), hq, d)
+        out[torch.from_numpy(r)] = o
+        lse[torch.from_numpy(r)] = (lse_nat * LOG2E).permute(1, 0, 2).reshape(len(r), hq)
+    return out.reshape(batch, seq_q, hq, d), lse.reshape(batch, seq_q, hq)
+
+
+def brute_force_attention(q, k, v, full_mask, window_size, *, cu_seqlens=None,
+                          sm_scale=None):
+    """Float64 pure-Python routed attention for tiny inputs.
+
+    Written from the definitions alone, independent of ``row_bounds``:
+    query i of a sequence may see key j of the same sequence iff ``j <= i``
+    (and ``j`` exists), and, when i is routed local, also ``i - j < W``
+    (F:145-155).  ``q``/``k``/``v`` are ``[B, S, H, D]`` arrays (converted to
+    float64); ``full_mask`` is ``[B, S]`` bool; ``cu_seqlens`` (B must be 1)
+    packs several sequences into the single batch row.
+    Returns (O ``[B, Sq, Hq, D]``, LSE2 ``[B, Sq, Hq]``) as float64 numpy.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    fm = np.asarray(full_mask, dtype=bool).reshape(q.shape[0], q.shape[1])
+    batch, seq_q, hq, d = q.shape
+    seq_kv, hkv = k.shape[1], k.shape[2]
+    g = hq // hkv
+    scale = (1.0 / d) ** 0.5 if sm_scale is None else float(sm_scale)
+    if cu_seqlens is None:
+        segs = [(0, seq_q, 0, seq_kv)]
+    else:
+        cu = [int(x) for x in cu_seqlens]
+        segs = [(cu[s], cu[s + 1], cu[s], cu[s + 1]) for s in range(len(cu) - 1)]
+    out = np.full((batch, seq_q, hq, d), np.nan)
+    lse = np.full((batch, seq_q, hq), np.nan)
+    for b in range(batch):
+        for (q0, q1, k0, k1) in segs:
+            for i in range(q1 - q0):
+                for h in range(hq):
+                    keys = [j for j in range(k1 - k0)
+                            if j <= i and (fm[b, q0 + i] or i - j < window_size)]
+                    if not keys:
+                        continue
+                    qi = q[b, q0 + i, h]
+                    sc = [scale * float(np.dot(qi, k[b, k0 + j, h // g])) for j in keys]
+                    mx = max(sc)
+                    w = [math.exp(x - mx) for x in sc]
+                    tot = sum(w)
+                    acc = np.zeros(d)
+                    for wj, j in zip(w, keys):
+                        acc += wj * v[b, k0 + j, h // g]
+                    out[b, q0 + i, h] = acc / tot
+                    lse[b, q0 + i, h] = (mx + math.log(tot)) * LOG2E
+    return out, lse
+
+
+def routed_flops(full_idx, local_idx, batch, seq_q, seq_kv, heads_q, head_dim,
+                 window_size, metadata=None) -> int:
+    """Algorithmic FLOPs of a routed prefill: ``4 * D * Hq * sum_rows |legal keys|``.
+
+    Two GEMMs (QK^T and PV) of ``2 * D`` FLOPs per legal (row, key, head).
+    Softmax work is not counted.
+    """
+    if metadata is None:
+        fs, ls, en = default_bounds(batch, seq_q, seq_kv, window_size)
+    else:
+        fs, ls, en = (np.asarray(metadata[n], dtype=np.int64)
+                      for n in ("full_starts", "local_starts", "causal_ends"))
+    start, end = row_bounds(full_idx, local_idx, fs, ls, en)
+    pairs = np.maximum(end - start, 0).sum()
+    return int(4 * head_dim * heads_q * int(pairs))

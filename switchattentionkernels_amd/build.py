@@ -1,0 +1,83 @@
+"""Build libswattn.so in-tree with hipcc for gfx950.
+
+``python -m switchattentionkernels_amd.build`` (or ``__graft_entry__.build()``)
+compiles every HIP source under ``csrc/`` into ``libswattn.so`` next to this
+file.  The library links against the HIP runtime that PyTorch-ROCm ships
+(``torch/lib/libamdhip64.so``) so that one process never holds two HIP
+runtimes; stream handles from ``torch.cuda.current_stream().cuda_stream``
+are then valid inside the library.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libswattn.so")
+ARCH = "gfx950"
+
+SOURCES = ["swattn_index.hip", "swattn_fwd.hip"]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found: install ROCm or set HIPCC")
+
+
+def _torch_lib_dir() -> str | None:
+    try:
+        import importlib.util
+        spec = importlib.util.find_spec("torch")
+        if spec is None or spec.origin is None:
+            return None
+        d = os.path.join(os.path.dirname(spec.origin), "lib")
+        return d if os.path.exists(os.path.join(d, "libamdhip64.so")) else None
+    except Exception:
+        return None
+
+
+def compile_flags() -> list[str]:
+    return [
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # Keep the compiler from forming packed fp32 instructions.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(ROOT, "include"),
+        "-I", CSRC,
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile ``libswattn.so``; returns its path.  Always recompiles."""
+    cmd = [_hipcc()] + compile_flags()
+    tl = _torch_lib_dir()
+    if tl is not None:
+        cmd += ["-L", tl, "-Wl,-rpath," + tl]
+    cmd += [os.path.join(CSRC, s) for s in SOURCES]
+    tmp = LIB + ".tmp"
+    cmd += ["-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(line for line in res.stderr.splitlines()
+                    if "packed-fp32-ops" not in line and line.strip())
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err:
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

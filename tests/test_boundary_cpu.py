@@ -1,0 +1,116 @@
+"""C-ABI and host-logic checks that need no GPU.
+
+The library must load and export every entry point that include/swattn.h
+declares, the ctypes signatures must match the header, and argument errors
+must be rejected on the host before anything touches a device.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import routing as R
+from switchattentionkernels_amd import _lib, routed_flops, workloads
+import switchattentionkernels_amd as sw
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "swattn.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*[\w\s\*]+?\b(swattn_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        out[m.group(1)] = len(args)
+    return out
+
+
+def test_library_exports_every_header_symbol():
+    funcs = _header_functions()
+    assert len(funcs) == 7, funcs
+    lib = _lib.lib()
+    for name in funcs:
+        assert hasattr(lib, name), name
+    assert set(funcs) == set(_lib.SIGNATURES)
+    for name, nargs in funcs.items():
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_version_and_workspace():
+    lib = _lib.lib()
+    assert lib.swattn_version() >= 1
+    assert lib.swattn_compact_workspace_bytes(16384) == 0
+    assert lib.swattn_compact_workspace_bytes(16385) == 2 * 4
+    assert lib.swattn_compact_workspace_bytes(65536) == 4 * 4
+
+
+def test_host_side_argument_errors():
+    lib = _lib.lib()
+    # head_dim != 128
+    st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, None, None, None, None, None,
+                                1, 1, 1, 1, 1, 64, 4, ctypes.c_float(1.0), None)
+    assert st == -1 and b"head_dim" in lib.swattn_last_error()
+    # heads_q not a multiple of heads_kv
+    st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, None, None, None, None, None,
+                                1, 1, 1, 6, 4, 128, 4, ctypes.c_float(1.0), None)
+    assert st == -1 and b"multiple" in lib.swattn_last_error()
+    # partial metadata
+    dummy = ctypes.c_void_p(16)
+    st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, dummy, None, None, None, None,
+                                1, 1, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None)
+    assert st == -1 and b"metadata" in lib.swattn_last_error()
+    # nothing to do is fine without touching the device
+    st = lib.swattn_prefill_fwd(None, None, None, None, 0, None, 0, None, None, None, None, None,
+                                1, 0, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None)
+    assert st == 0
+    assert lib.swattn_compact(None, -1, None, None, None, 0, None) == -1
+    assert lib.swattn_check_indices(None, -1, None, 0, 5, None, None) == -1
+    assert lib.swattn_build_metadata(None, None, 1, 4, 4, 0, *([None] * 7), None) == -1
+
+
+def test_api_rejects_cpu_and_dtype_errors_like_the_reference():
+    q = torch.zeros(1, 8, 4, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    idx = torch.arange(8, dtype=torch.int32)
+    with pytest.raises(TypeError, match="requires BF16"):
+        sw.switch_gqa_prefill_forward(q.float(), k, k, idx, idx[:0])
+    with pytest.raises(ValueError, match="supported accelerator device"):
+        sw.switch_gqa_prefill_forward(q, k, k, idx, idx[:0])
+    with pytest.raises(TypeError, match="device-resident bool tensor"):
+        sw.build_switch_query_indices(torch.zeros(8, dtype=torch.bool))
+    with pytest.raises(ValueError, match="supported accelerator device"):
+        sw.build_switch_attention_metadata(8, 8, device="cpu", window_size=4)
+
+
+def test_package_flops_equal_oracle_flops():
+    gen = torch.Generator().manual_seed(0)
+    for b, s, w, p in ((1, 300, 64, 0.3), (2, 129, 7, 0.5), (1, 50, 100, 1.0)):
+        m = torch.rand(b, s, generator=gen) < p
+        f, l = R.compact(m.numpy())
+        got = routed_flops(torch.from_numpy(f), torch.from_numpy(l), batch=b, seq_q=s, seq_kv=s,
+                           heads_q=8, head_dim=128, window=w)
+        assert got == oracle.routed_flops(f, l, b, s, s, 8, 128, w)
+
+
+def test_workloads_are_seeded_and_shaped():
+    a = workloads.build("cpu", seed=3)
+    b = workloads.build("cpu", seed=3)
+    assert torch.equal(a["q"], b["q"]) and torch.equal(a["mask"], b["mask"])
+    assert a["q"].shape == (1, 1024, 8, 128) and a["k"].shape == (1, 1024, 2, 128)
+    gen = torch.Generator().manual_seed(0)
+    mk = workloads.markov_mask(gen, 200000, 0.3)
+    assert abs(mk.float().mean().item() - 0.3) < 0.02
+    runs = (mk[1:] != mk[:-1]).sum().item()
+    assert runs < 200000 * 0.05          # clustered: few switches
+    rp = workloads.ramp_mask(gen, 200000)
+    assert abs(rp.float().mean().item() - 0.15) < 0.01
+    assert rp[:20000].float().mean() < rp[-20000:].float().mean()
+    vl = workloads.varlen_lengths(torch.Generator().manual_seed(1))
+    assert len(vl) == 8 and all(512 <= x <= 8192 for x in vl)

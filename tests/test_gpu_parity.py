@@ -1,0 +1,378 @@
+"""GPU parity: libswattn.so (through the public API and the C ABI) vs the CPU oracle.
+
+Bars:
+* compaction index lists: bit-exact (torch.equal);
+* O: max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle (bf16 output);
+* LSE (log2): |delta| <= 1e-3 * max(1, |ref|)  (relative 1e-3 with an absolute
+  floor, because LSE can be ~0 at position 0).
+Full-size configs are checked on sampled rows against the oracle plus
+size-independent properties that must hold bit-exactly.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import routing as R
+from switchattentionkernels_amd import (
+    build_switch_attention_metadata,
+    build_switch_query_indices,
+    switch_gqa_prefill_forward,
+    switch_gqa_prefill_varlen_forward,
+    workloads,
+)
+from switchattentionkernels_amd import _lib
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+O_MAX, O_MEAN, LSE_REL = 2e-2, 2e-3, 1e-3
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _qkv(seed, b, s, hq, hkv, skv=None, scale=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    return workloads.make_qkv(gen, b, s, s if skv is None else skv, hq, hkv, 128, scale)
+
+
+def _mask(seed, shape, p):
+    gen = torch.Generator().manual_seed(seed + 7)
+    return torch.rand(shape, generator=gen) < p
+
+
+def _gpu_run(q, k, v, mask, window, metadata=None, **kw):
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
+                                        window_size=window, metadata=metadata, **kw)
+    torch.cuda.synchronize()
+    return o, lse, full, local
+
+
+def _assert_close(o, lse, o_ref, lse_ref, rows=None, tag=""):
+    o = o.float().cpu().reshape(-1, *o.shape[2:])
+    lse = lse.cpu().reshape(-1, lse.shape[-1])
+    o_ref = o_ref.reshape(-1, *o_ref.shape[2:])
+    lse_ref = lse_ref.reshape(-1, lse_ref.shape[-1])
+    if rows is not None:
+        r = torch.as_tensor(rows)
+        o, lse, o_ref, lse_ref = o[r], lse[r], o_ref[r], lse_ref[r]
+    err = (o - o_ref).abs()
+    assert torch.isfinite(o).all(), f"{tag}: non-finite output"
+    mx, mean = err.max().item(), err.mean().item()
+    lerr = ((lse - lse_ref).abs() / lse_ref.abs().clamp(min=1.0)).max().item()
+    print(f"{tag}: O max {mx:.3e} mean {mean:.3e}  LSE rel {lerr:.3e}", flush=True)
+    assert mx <= O_MAX, f"{tag}: O max-abs {mx}"
+    assert mean <= O_MEAN, f"{tag}: O mean-abs {mean}"
+    assert lerr <= LSE_REL, f"{tag}: LSE rel {lerr}"
+
+
+def _oracle(q, k, v, mask, window, metadata=None, rows=None, sm_scale=None):
+    full, local = R.compact(mask.numpy())
+    md = None
+    if metadata is not None:
+        md = {n: getattr(metadata, n).cpu().numpy() for n in
+              ("full_starts", "local_starts", "causal_ends")}
+    return oracle.routed_attention(q, k, v, full, local, window_size=window, metadata=md,
+                                   rows=rows, sm_scale=sm_scale)
+
+
+def _sample_rows(n, count, seed):
+    gen = torch.Generator().manual_seed(seed)
+    r = torch.randperm(n, generator=gen)[:count]
+    edge = torch.tensor([0, 1, 63, 64, 65, n // 2, n - 2, n - 1]).clamp(0, n - 1)
+    return torch.unique(torch.cat([r, edge])).numpy()
+
+
+# ----------------------------------------------------------------------------
+# compaction
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,p", [(1, 0.5), (1, 1.0), (63, 0.5), (64, 0.0), (65, 1.0),
+                                 (1000, 0.25), (16384, 0.25), (16385, 0.5), (65536, 0.15),
+                                 (100003, 0.7)])
+def test_compact_bit_exact(n, p):
+    m = _mask(n, (n,), p)
+    full, local = build_switch_query_indices(m.to(DEV))
+    pos = torch.arange(n, dtype=torch.int32, device=DEV)
+    md = m.to(DEV)
+    assert full.dtype == torch.int32 and local.dtype == torch.int32
+    assert torch.equal(full, pos[md]) and torch.equal(local, pos[~md])
+    f_o, l_o = R.compact(m.numpy())
+    assert np.array_equal(full.cpu().numpy(), f_o) and np.array_equal(local.cpu().numpy(), l_o)
+
+
+def test_compact_patterns_and_2d():
+    for m in (torch.arange(5000) % 2 == 0, torch.arange(5000) % 64 == 0,
+              torch.ones(70000, dtype=torch.bool), torch.zeros(70000, dtype=torch.bool)):
+        full, local = build_switch_query_indices(m.to(DEV))
+        f_o, l_o = R.compact(m.numpy())
+        assert np.array_equal(full.cpu().numpy(), f_o)
+        assert np.array_equal(local.cpu().numpy(), l_o)
+    m2 = _mask(5, (3, 777), 0.3)
+    full, local = build_switch_query_indices(m2.to(DEV))
+    f_o, l_o = R.compact(m2.numpy())
+    assert np.array_equal(full.cpu().numpy(), f_o) and np.array_equal(local.cpu().numpy(), l_o)
+    full1, _ = build_switch_query_indices(m2[:1].to(DEV))
+    assert np.array_equal(full1.cpu().numpy(), R.compact(m2[:1].numpy())[0])
+
+
+# ----------------------------------------------------------------------------
+# validation: same exceptions and messages as the reference
+# ----------------------------------------------------------------------------
+
+def test_index_validation_errors():
+    q, k, v = (t.to(DEV) for t in _qkv(1, 1, 7, 4, 2))
+    ok_f, ok_l = [0, 3, 5], [1, 2, 4, 6]
+    cases = [([0, 3, 7], ok_l), ([-1, 3, 5], ok_l), ([3, 0, 5], ok_l), ([0, 3, 3], ok_l),
+             (ok_f, [1, 2, 4, 9]), (ok_f, [2, 1, 4, 6]), (ok_f, [1, 2, 3, 6]),
+             (ok_f, [1, 2, 4]), ([3, 0, 5], [9, 1, 2, 4])]
+    for f, lo in cases:
+        exc, msg = R.first_error(np.array(f), np.array(lo), 7)
+        with pytest.raises(exc, match=re.escape(msg)):
+            switch_gqa_prefill_forward(q, k, v, torch.tensor(f, device=DEV),
+                                       torch.tensor(lo, device=DEV), window_size=4)
+    # valid lists in other dtypes / shapes are accepted (V:277-283 casts to int32)
+    o, lse = switch_gqa_prefill_forward(q, k, v, torch.tensor([ok_f], device=DEV),
+                                        torch.tensor(ok_l, dtype=torch.int64, device=DEV),
+                                        window_size=4)
+    assert o.shape == q.shape and lse.shape == q.shape[:3]
+    with pytest.raises(ValueError, match="one batch of query indices"):
+        switch_gqa_prefill_forward(q, k, v, torch.tensor([ok_f, ok_f], device=DEV),
+                                   torch.tensor(ok_l, device=DEV))
+    with pytest.raises(ValueError, match="supported accelerator device"):
+        switch_gqa_prefill_forward(q, k, v, torch.tensor(ok_f), torch.tensor(ok_l, device=DEV))
+    with pytest.raises(ValueError, match="window_size must be positive"):
+        switch_gqa_prefill_forward(q, k, v, torch.tensor(ok_f, device=DEV),
+                                   torch.tensor(ok_l, device=DEV), window_size=0)
+    for kw, msg in (({"block_m": 128}, "BM64"), ({"block_k": 32}, "BK64"),
+                    ({"num_stages": 2}, "one stage"), ({"threads": 256}, "128 threads")):
+        with pytest.raises(AssertionError, match=msg):
+            switch_gqa_prefill_forward(q, k, v, torch.tensor(ok_f, device=DEV),
+                                       torch.tensor(ok_l, device=DEV), **kw)
+    with pytest.raises(TypeError, match="device-resident bool"):
+        build_switch_query_indices(torch.zeros(4, dtype=torch.int32, device=DEV))
+
+
+def test_metadata_validation_errors():
+    q, k, v = (t.to(DEV) for t in _qkv(2, 1, 16, 4, 2))
+    md = build_switch_attention_metadata(16, 16, device=q.device, window_size=4)
+    f, l = build_switch_query_indices(_mask(2, (16,), 0.5).to(DEV))
+    bad = md.__class__(**{**md.__dict__, "causal_ends": md.causal_ends[:15]})
+    with pytest.raises(ValueError, match="invalid Switch Attention position metadata"):
+        switch_gqa_prefill_forward(q, k, v, f, l, metadata=bad)
+    bad = md.__class__(**{**md.__dict__, "full_starts": md.full_starts.long()})
+    with pytest.raises(ValueError, match="invalid Switch Attention position metadata"):
+        switch_gqa_prefill_forward(q, k, v, f, l, metadata=bad)
+
+
+# ----------------------------------------------------------------------------
+# metadata builder
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cu,w", [([0, 37], 5), ([0, 5, 5, 12, 300], 4), ([0, 1, 2, 3], 1),
+                                  ([0, 1000, 1513, 4000], 256)])
+def test_metadata_matches_oracle(cu, w):
+    md = build_switch_attention_metadata(cu[-1], cu[-1], device=DEV, window_size=w, cu_seqlens=cu)
+    ref = R.varlen_metadata(cu, cu, w)
+    for name, arr in ref.items():
+        got = getattr(md, name)
+        assert got.dtype == torch.int32 and got.is_contiguous() and got.ndim == 1
+        assert np.array_equal(got.cpu().numpy(), arr), name
+
+
+def test_metadata_distinct_kv_offsets():
+    cq, ck = [0, 10, 30], [0, 25, 40]
+    md = build_switch_attention_metadata(30, 40, device=DEV, window_size=3, cu_seqlens=cq,
+                                         cu_seqlens_kv=ck)
+    ref = R.varlen_metadata(cq, ck, 3)
+    for name, arr in ref.items():
+        assert np.array_equal(getattr(md, name).cpu().numpy(), arr), name
+
+
+# ----------------------------------------------------------------------------
+# forward: small shapes and edge cases, every row against the oracle
+# ----------------------------------------------------------------------------
+
+SMALL = [
+    # (b, s, hq, hkv, w, p, skv)
+    (1, 1, 4, 1, 1, 1.0, None),        # length-1 sequence
+    (1, 37, 4, 4, 8, 0.5, None),       # G=1, count < 64
+    (1, 100, 8, 2, 1, 0.3, None),      # W = 1
+    (1, 200, 8, 2, 512, 0.3, None),    # W >= S
+    (1, 333, 10, 2, 64, 0.4, None),    # G=5, S not a multiple of 64
+    (1, 257, 8, 1, 33, 0.2, None),     # G=8
+    (2, 190, 8, 2, 50, 0.25, None),    # B > 1
+    (1, 500, 4, 1, 100, 0.0, None),    # pure local
+    (1, 500, 4, 1, 100, 1.0, None),    # pure full
+    (1, 150, 4, 2, 40, 0.5, 400),      # Skv > Sq (top-left alignment, F:154)
+    (1, 150, 4, 2, 40, 0.5, 90),       # Skv < Sq
+    (3, 64, 32, 8, 16, 0.5, None),     # Hq32/Hkv8, exact tiles
+]
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,skv", SMALL)
+def test_forward_small(b, s, hq, hkv, w, p, skv):
+    q, k, v = _qkv(s * 7 + hq, b, s, hq, hkv, skv)
+    m = _mask(s, (b, s), p)
+    o, lse, _, _ = _gpu_run(q, k, v, m, w)
+    o_ref, lse_ref = _oracle(q, k, v, m, w)
+    _assert_close(o, lse, o_ref, lse_ref, tag=f"b{b} s{s} {hq}/{hkv} w{w} p{p} skv{skv}")
+
+
+def test_forward_custom_scale():
+    q, k, v = _qkv(3, 1, 300, 8, 2)
+    m = _mask(3, (1, 300), 0.3)
+    o, lse, _, _ = _gpu_run(q, k, v, m, 64, sm_scale=0.02)
+    o_ref, lse_ref = _oracle(q, k, v, m, 64, sm_scale=0.02)
+    _assert_close(o, lse, o_ref, lse_ref, tag="sm_scale=0.02")
+
+
+def test_cpu_config_every_row():
+    wl = workloads.build("cpu", seed=0)
+    o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
+    o_ref, lse_ref = _oracle(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
+    _assert_close(o, lse, o_ref, lse_ref, tag="config cpu")
+
+
+@pytest.mark.parametrize("p", [0.0, 0.25, 1.0])
+def test_b2_config(p):
+    wl = workloads.build("b2", seed=1, p_full=p)
+    o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
+    rows = _sample_rows(2 * 4096, 1500, 1)
+    o_ref, lse_ref = _oracle(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"], rows=rows)
+    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag=f"config b2 p{p}")
+
+
+def test_varlen_config():
+    wl = workloads.build("varlen", seed=2)
+    cu = wl["cu_seqlens"]
+    full, local = build_switch_query_indices(wl["mask"].to(DEV))
+    o, lse = switch_gqa_prefill_varlen_forward(wl["q"].to(DEV), wl["k"].to(DEV), wl["v"].to(DEV),
+                                               full, local, cu, window_size=wl["window"])
+    torch.cuda.synchronize()
+    md = R.varlen_metadata(cu, cu, wl["window"])
+    rows = _sample_rows(cu[-1], 600, 2)
+    rows = np.unique(np.concatenate([rows, np.array(cu[1:-1]), np.array(cu[1:-1]) - 1]))
+    f_o, l_o = R.compact(wl["mask"].numpy())
+    o_ref, lse_ref = oracle.routed_attention(wl["q"], wl["k"], wl["v"], f_o, l_o,
+                                             metadata=md, rows=rows)
+    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag="config varlen")
+
+
+@pytest.mark.parametrize("p", [0.1, 0.25, 0.5])
+def test_s16k_config_sampled(p):
+    wl = workloads.build("s16k", seed=3, p_full=p)
+    o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
+    rows = _sample_rows(16384, 300, 3)
+    o_ref, lse_ref = _oracle(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"], rows=rows)
+    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag=f"config s16k p{p}")
+
+
+def test_s64k_config_sampled():
+    wl = workloads.build("s64k", seed=4)
+    o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
+    rows = _sample_rows(65536, 120, 4)
+    o_ref, lse_ref = _oracle(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"], rows=rows)
+    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag="config s64k")
+
+
+# ----------------------------------------------------------------------------
+# size-independent properties at full size (bit-exact)
+# ----------------------------------------------------------------------------
+
+def test_routed_equals_rowwise_select_s16k():
+    """Each row depends only on its own route: routed == where(mask, all-full, all-local)."""
+    wl = workloads.build("s16k", seed=5, p_full=0.25)
+    m = wl["mask"]
+    o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], m, 1024)
+    o_f, lse_f, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], torch.ones_like(m), 1024)
+    o_l, lse_l, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], torch.zeros_like(m), 1024)
+    md = m.to(DEV)
+    assert torch.equal(o, torch.where(md[..., None, None], o_f, o_l))
+    assert torch.equal(lse, torch.where(md[..., None], lse_f, lse_l))
+
+
+def test_batch_rows_independent_bit_exact():
+    q, k, v = _qkv(6, 3, 1000, 8, 2)
+    m = _mask(6, (3, 1000), 0.3)
+    o, lse, _, _ = _gpu_run(q, k, v, m, 128)
+    for b in range(3):
+        ob, lb, _, _ = _gpu_run(q[b:b + 1], k[b:b + 1], v[b:b + 1], m[b:b + 1], 128)
+        assert torch.equal(o[b:b + 1], ob) and torch.equal(lse[b:b + 1], lb)
+
+
+def test_packed_equals_per_sequence_bit_exact():
+    cu = [0, 700, 701, 2000, 2345]
+    q, k, v = _qkv(7, 1, 2345, 8, 2)
+    m = _mask(7, (1, 2345), 0.3)
+    full, local = build_switch_query_indices(m.to(DEV))
+    o, lse = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local, cu,
+                                               window_size=100)
+    for a, b in zip(cu[:-1], cu[1:]):
+        os_, ls_, _, _ = _gpu_run(q[:, a:b], k[:, a:b], v[:, a:b], m[:, a:b], 100)
+        assert torch.equal(o[:, a:b], os_) and torch.equal(lse[:, a:b], ls_)
+
+
+def test_default_equals_explicit_metadata_bit_exact():
+    q, k, v = _qkv(8, 1, 3000, 8, 2)
+    m = _mask(8, (1, 3000), 0.4)
+    o, lse, _, _ = _gpu_run(q, k, v, m, 300)
+    md = build_switch_attention_metadata(3000, 3000, device=DEV, window_size=300)
+    o2, lse2, _, _ = _gpu_run(q, k, v, m, 300, metadata=md)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+
+
+def test_deterministic():
+    q, k, v = _qkv(9, 1, 4096, 32, 8)
+    m = _mask(9, (1, 4096), 0.25)
+    a = _gpu_run(q, k, v, m, 1024)
+    b = _gpu_run(q, k, v, m, 1024)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_c_abi_writes_only_listed_rows():
+    """Through the C ABI: rows in neither list keep their prior contents."""
+    q, k, v = (t.to(DEV) for t in _qkv(10, 1, 300, 8, 2))
+    m = _mask(10, (300,), 0.5).to(DEV)
+    full, local = build_switch_query_indices(m)
+    out = torch.full_like(q, 7.0)
+    lse = torch.full(q.shape[:3], -3.0, device=DEV)
+    L = _lib.lib()
+    st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(),
+                              full.numel(), None, 0, None, None, None, out.data_ptr(),
+                              lse.data_ptr(), 1, 300, 300, 8, 2, 128, 64,
+                              ctypes.c_float(128 ** -0.5 * oracle.LOG2E),
+                              _lib.stream_handle(q.device))
+    assert st == 0
+    torch.cuda.synchronize()
+    lm = ~m
+    assert (out[0][lm] == 7.0).all() and (lse[0][lm] == -3.0).all()
+    assert not (out[0][m] == 7.0).all()
+    ref_o, ref_l = switch_gqa_prefill_forward(q, k, v, full, local, window_size=64)
+    assert torch.equal(out[0][m], ref_o[0][m]) and torch.equal(lse[0][m], ref_l[0][m])
+
+
+# ----------------------------------------------------------------------------
+# committed golden fixtures
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
+def test_golden_fixture(name):
+    z = np.load(os.path.join(GOLDEN, name))
+    bf = lambda a: torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16)  # noqa: E731
+    q, k, v = bf(z["q"]), bf(z["k"]), bf(z["v"])
+    m = torch.from_numpy(z["mask"])
+    w = int(z["window"])
+    if "cu_seqlens" in z.files:
+        full, local = build_switch_query_indices(m.to(DEV))
+        o, lse = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
+                                                   z["cu_seqlens"].tolist(), window_size=w)
+    else:
+        o, lse, full, local = _gpu_run(q, k, v, m, w)
+    assert np.array_equal(full.cpu().numpy(), z["full_idx"])
+    assert np.array_equal(local.cpu().numpy(), z["local_idx"])
+    _assert_close(o, lse, torch.from_numpy(z["out"]), torch.from_numpy(z["lse"]), tag=name)
