@@ -11,25 +11,38 @@
 // only to the routed rows (V:243-249).
 //
 // Design (MI355X-first, not a translation of the TileLang schedule):
-// * Work item = (branch, tile of 128 "rows", KV head).  A row is a
-//   (compacted query slot, query head of the KV head's group) pair with the head
-//   index fastest, so one K/V tile in LDS serves every query head of the group
-//   (GQA packing) and a wave's 32 rows span only 32/G query positions.
+// * Work item = (branch, tile of 256 "rows", KV head).  A row is a
+//   (compacted query slot, query head of the KV head's group) pair with the
+//   head index fastest, so one K/V tile in LDS serves every query head of the
+//   group (GQA packing) and a wave's rows span only 64/G query positions.
 // * The whole routed problem is one grid: full-branch tiles first, last tile
 //   (longest causal prefix) first, then local tiles; KV head = item % Hkv so
 //   that with Hkv = 8 every XCD (blockIdx % 8) streams a single KV head
 //   through its own L2.  Counts come from the index lists' lengths, so new
 //   routing never recompiles anything.
-// * Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (Q^T is held
-//   in registers as the B operand), so every lane owns one query row and 32
-//   keys of the 64-key tile: row max / row sum are lane-local plus one
-//   permlane32 swap.  The S^T accumulator is already the B operand of
-//   O^T = V^T P^T (keys permuted consistently on both sides), and V^T operands
-//   come straight from the row-major V tile with ds_read_b64_tr_b16.
-// * K/V tiles are double-buffered in LDS (register-staged prefetch of tile
-//   j+1 during tile j, one barrier per tile); K tiles outside a wave's key
-//   range are skipped, interior tiles skip the mask, and the O rescale is
-//   skipped when no row's max moved.
+// * Eight waves share each K/V tile; each wave owns 32 rows and computes
+//   S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (Q^T stays in registers as the
+//   B operand).  Two waves per SIMD let one wave's softmax (VALU) run under
+//   the other's MFMAs, and every accumulator stays in ordinary VGPRs.  Each
+//   lane owns one query row and 32 keys of the 64-key tile: row max and row
+//   sum are lane-local plus one permlane32 swap.  The S^T accumulator is
+//   already the B operand of O^T = V^T P^T (keys permuted consistently on
+//   both sides), and V^T operands come straight from the row-major V tile
+//   with ds_read_b64_tr_b16.
+// * K/V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
+//   staging) through three LDS stages, two tiles ahead of the compute, with
+//   one barrier per tile.  The loads are issued from inline assembly and
+//   waited for with explicit vmcnt counts: the compiler cannot see that they
+//   target another stage than the one being read, and would otherwise drain
+//   every load before each LDS read.  LDS rows are unpadded 256-byte rows
+//   whose 16-byte chunks are XOR-swizzled so both operand read patterns are
+//   conflict-free.
+// * The running max is only moved when it grows by more than 2^8 in the
+//   exp2 domain (rescaling O is then rare); P = 2^(s*c - m*c) stays below
+//   2^8, and O = acc / l, LSE = log2(l) + m*c are the same quantities as with
+//   an exact running max.
+// * Tiles outside a wave's key range are skipped and interior tiles skip the
+//   mask.
 
 #include <limits.h>
 #include <math.h>
@@ -47,14 +60,17 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kD = 128;                               // head_dim
 constexpr int kBN = 64;                               // keys per K/V tile
-constexpr int kWaves = 4;                             // waves per workgroup
+constexpr int kWaves = 8;                             // waves per workgroup
 constexpr int kThreads = kWaves * 64;
-constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerItem = kWaves * kRowsPerWave;   // 128 rows per work item
-constexpr int kRowBytes = 288;                        // LDS bytes per key row: 256 + 32 pad
-constexpr int kTileBytes = kBN * kRowBytes;           // one K or V tile
+constexpr int kRowsPerWave = 32;                      // one 32-row MFMA block
+constexpr int kRowsPerItem = kWaves * kRowsPerWave;   // 256 rows per work item
+constexpr int kRowBytes = kD * 2;                     // 256-byte key rows, unpadded
+constexpr int kTileBytes = kBN * kRowBytes;           // one K or V tile: 16 KiB
 constexpr int kStageBytes = 2 * kTileBytes;           // K + V
-constexpr int kLdsBytes = 2 * kStageBytes;            // double buffered
+constexpr int kStages = 3;
+constexpr int kLdsBytes = kStages * kStageBytes;      // 96 KiB
+constexpr int kLoadsPerTile = 4;                      // global_load_lds per thread per tile
+static_assert(kLoadsPerTile == 4, "the vmcnt(4) waits in fwd_kernel assume 4 loads per tile");
 constexpr float kMaxSentinel = -1073741824.0f;        // -2^30 (V:174)
 
 struct FwdParams {
@@ -72,6 +88,13 @@ struct FwdParams {
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
 };
+
+// Chunk swizzle: logical 16-byte chunk j of key row r lives at chunk
+// j ^ swz(r).  swz is a permutation of r mod 16, so 16 lanes reading one
+// chunk of 16 consecutive rows hit 16 distinct bank groups, and the four
+// rows x four chunks touched by 32 lanes of a transposing V read are 16
+// distinct chunks as well.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 __device__ __forceinline__ float xor32_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -100,11 +123,102 @@ __device__ __forceinline__ i16x4 lds_tr16(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (lds_i16x4*)((__attribute__((address_space(3))) char*)(p)));
 }
+// 16 bytes per lane from global memory to LDS at lds_base + 16 * lane
+// (global_load_lds_dwordx4; the LDS base goes through M0 and must be
+// wave-uniform).  Issued as inline assembly so that the compiler's wait
+// insertion does not treat it as a store that aliases every LDS read.
+__device__ __forceinline__ void dma16(const uint16_t* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(lds_base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+
+// Stage one 64-key K and V tile: wave w fills key rows 8w .. 8w+7.  Load i
+// of a wave writes rows 8w+4i .. +3 (1 KiB, lane-linear); lane l lands on
+// chunk position l%16 of row l/16 and therefore fetches logical chunk
+// (l%16) ^ swz(row) from global memory.  Issues kLoadsPerTile loads per lane.
+__device__ __forceinline__ void stage_tile(const FwdParams& p, const char* stage, int key0,
+                                           int kvh, int wave, int lane) {
+  const int sub = lane >> 4, pcol = lane & 15;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(stage) + 8 * wave * kRowBytes);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * wave + 4 * i + sub;
+    const int j = pcol ^ swz(row);
+    const int key = min(key0 + row, p.total_kv - 1);
+    const int64_t off = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 8 * j;
+    dma16(p.k + off, base + 4 * i * kRowBytes);
+    dma16(p.v + off, base + 4 * i * kRowBytes + kTileBytes);
+  }
+}
+
+template <bool kMeta>
+__device__ __forceinline__ void row_bounds(const FwdParams& p, int branch, int pos, int& ks,
+                                           int& ke) {
+  if constexpr (kMeta) {
+    ks = p.starts[branch][pos];
+    ke = p.ends[pos];
+  } else {
+    const int b = pos / p.seq_q;
+    const int i = pos - b * p.seq_q;
+    const int base = b * p.seq_kv;
+    ke = base + min(i + 1, p.seq_kv);
+    ks = branch == 0 ? base : base + max(i - p.window + 1, 0);
+  }
+  ks = max(ks, 0);
+  ke = min(ke, p.total_kv);
+}
+
+// Keys held by this lane in a 32-key S^T block: 8*j + 4*hh + i (register 4j+i).
+__device__ __forceinline__ void mask_block(f32x16& s, int key0, int hh, int ks, int ke) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = key0 + 8 * j + 4 * hh + i;
+      if (key < ks || key >= ke) s[4 * j + i] = -INFINITY;
+    }
+  }
+}
+
+// Online-softmax step of one 32-row x 64-key tile held as two S^T blocks.
+// The max m only moves when the tile max exceeds it by more than 8 in the
+// exp2 domain (or m is still the sentinel); alpha is then the O rescale
+// factor, otherwise exactly 1.  Overwrites s0/s1 with P = 2^(s*c - m*c)
+// (fp32) and returns whether m moved.
+__device__ __forceinline__ bool softmax_step(f32x16& s0, f32x16& s1, float& m, float& l, float c,
+                                             float& alpha) {
+  float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+  for (int e = 1; e < 16; ++e) mx = fmaxf(mx, fmaxf(s0[e], s1[e]));
+  mx = xor32_max(mx);
+  const bool moved = (mx - m) * c > 8.0f;
+  const float m_new = moved ? mx : m;
+  alpha = moved ? __builtin_amdgcn_exp2f((m - m_new) * c) : 1.0f;
+  const float mc = m_new * c;
+  float rs0 = 0.f, rs1 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    s0[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[e], c, -mc));
+    s1[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[e], c, -mc));
+    rs0 += s0[e];
+    rs1 += s1[e];
+  }
+  const float rs = xor32_sum(rs0 + rs1);
+  l = l * alpha + rs;
+  m = m_new;
+  return moved;
+}
 
 template <bool kMeta>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void fwd_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
   __shared__ int s_range[2 * kWaves];
 
   const int tid = threadIdx.x;
@@ -124,22 +238,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   // ---- this lane's row ------------------------------------------------------
   const int r = tile * kRowsPerItem + wave * kRowsPerWave + rl;
   const int slot = r / G;
-  const int hg = r - slot * G;
+  const int qh = kvh * G + (r - slot * G);
   const bool valid = slot < count;
   const int pos = idx[valid ? slot : count - 1];
   int ks, ke;
-  if constexpr (kMeta) {
-    ks = p.starts[branch][pos];
-    ke = p.ends[pos];
-  } else {
-    const int b = pos / p.seq_q;
-    const int i = pos - b * p.seq_q;
-    const int base = b * p.seq_kv;
-    ke = base + min(i + 1, p.seq_kv);
-    ks = branch == 0 ? base : base + max(i - p.window + 1, 0);
-  }
-  ks = max(ks, 0);
-  ke = min(ke, p.total_kv);
+  row_bounds<kMeta>(p, branch, pos, ks, ke);
 
   // ---- key ranges: wave union / intersection, workgroup union --------------
   const int w_min_s = wave_min(valid ? ks : INT_MAX);
@@ -160,60 +263,49 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int t_begin = g_s / kBN;
   const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : t_begin;
 
-  // ---- Q rows as MFMA B operands (Q^T[d][row]) -------------------------------
-  const int qh = kvh * G + hg;
+  // ---- Q row as MFMA B operands (Q^T[d][row]); wait before any LDS load -----
   bf16x8 qf[8];
   {
     const uint16_t* qrow = p.q + (static_cast<int64_t>(pos) * p.hq + qh) * kD + 8 * hh;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- K/V staging: thread -> 16-byte chunk cc of keys 4*kq .. 4*kq+3 ------
-  const int cc = tid & 15;
-  const int kq = tid >> 4;
-  uint4 kr[4], vr[4];
-  auto gload = [&](int tk) {
-    const int key0 = tk * kBN + 4 * kq;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int key = min(key0 + e, p.total_kv - 1);
-      const int64_t off = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 8 * cc;
-      kr[e] = *reinterpret_cast<const uint4*>(p.k + off);
-      vr[e] = *reinterpret_cast<const uint4*>(p.v + off);
-    }
-  };
-  auto lstore = [&](int stage) {
-    char* kb = smem + stage * kStageBytes;
-    char* vb = kb + kTileBytes;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      *reinterpret_cast<uint4*>(kb + (4 * kq + e) * kRowBytes + 16 * cc) = kr[e];
-      *reinterpret_cast<uint4*>(vb + (4 * kq + e) * kRowBytes + 16 * cc) = vr[e];
-    }
-  };
+  // ---- prologue: two tiles in flight -----------------------------------------
+  if (t_begin < t_end) stage_tile(p, smem, t_begin * kBN, kvh, wave, lane);
+  if (t_begin + 1 < t_end) stage_tile(p, smem + kStageBytes, (t_begin + 1) * kBN, kvh, wave, lane);
 
   f32x16 o[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) o[d] = f32x16{};
   float m = kMaxSentinel, l = 0.f;
   const float c = p.c;
+  bool o_zero = true;  // O is still exactly zero: a rescale can be skipped
 
-  // Per-lane LDS offsets.
-  const int k_off = rl * kRowBytes + 16 * hh;
+  // Per-lane LDS byte offsets inside a stage.
+  // K operand (A of S^T): key row 32*kb + rl, logical chunk 2*kk + hh.
+  const int kx = hh ^ swz(rl);
+  // V operand (A of O^T, transposing read): key rows 16*s2 + vrow (+8),
+  // logical chunk 4*d + cq, 8-byte half (lane & 1).
   const int g16 = lane >> 4, i16 = lane & 15;
-  const int v_off = (4 * hh + (i16 >> 2)) * kRowBytes + 2 * (16 * (g16 & 1) + 4 * (i16 & 3));
+  const int cq = 2 * (g16 & 1) + ((i16 & 3) >> 1);
+  const int vrow = 4 * hh + (i16 >> 2);
+  const int vsw0 = swz(vrow), vsw1 = swz(vrow + 8);
 
-  if (t_end > t_begin) {
-    gload(t_begin);
-    lstore(0);
-  }
-  __syncthreads();
-
+  int stage = 0;
   for (int tk = t_begin; tk < t_end; ++tk) {
-    const int stage = (tk - t_begin) & 1;
-    const bool more = tk + 1 < t_end;
-    if (more) gload(tk + 1);
+    // This lane's loads of tile tk are the oldest outstanding ones; after the
+    // barrier every lane's are, and every wave has finished reading the stage
+    // that the loads issued next will overwrite.
+    if (tk + 1 < t_end)
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (tk + 2 < t_end) {
+      const int s2i = stage == 0 ? 2 : stage - 1;
+      stage_tile(p, smem + s2i * kStageBytes, (tk + 2) * kBN, kvh, wave, lane);
+    }
     const int key0 = tk * kBN;
     if (key0 < w_max_e && key0 + kBN > w_min_s) {
       const char* kb = smem + stage * kStageBytes;
@@ -222,47 +314,25 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
       f32x16 s0 = f32x16{}, s1 = f32x16{};
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kb + k_off + 32 * kk);
-        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kb + k_off + 32 * kRowBytes + 32 * kk);
+        const int off = rl * kRowBytes + (((2 * kk) ^ kx) << 4);
+        const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kb + off);
+        const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kb + off + 32 * kRowBytes);
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk], s1, 0, 0, 0);
       }
-      // Mask only tiles that are not interior for every row of this wave.
       if (!(key0 >= w_max_s && key0 + kBN <= w_min_e)) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 8 * j + 4 * hh + i;
-            if (key < ks || key >= ke) s0[4 * j + i] = -INFINITY;
-            if (key + 32 < ks || key + 32 >= ke) s1[4 * j + i] = -INFINITY;
-          }
-        }
+        mask_block(s0, key0, hh, ks, ke);
+        mask_block(s1, key0 + 32, hh, ks, ke);
       }
-      // Online softmax (base 2), lane-local plus one cross-half exchange.
-      float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, fmaxf(s0[e], s1[e]));
-      mx = xor32_max(mx);
-      const float m_new = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f((m - m_new) * c);
-      const float mc = m_new * c;
-      float rs = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s0[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[e], c, -mc));
-        s1[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[e], c, -mc));
-        rs += s0[e] + s1[e];
-      }
-      rs = xor32_sum(rs);
-      l = l * alpha + rs;
-      m = m_new;
-      if (wave_ballot(alpha != 1.0f)) {
+      float alpha;
+      const bool moved = softmax_step(s0, s1, m, l, c, alpha);
+      if (!o_zero && wave_ballot(moved)) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[d] *= alpha;
       }
-      // P^T as B operands: k-step s2 covers keys 16*s2 .. 16*s2+15, and this
-      // lane's element t is key 16*s2 + 8*(t>>2) + 4*hh + (t&3).
+      o_zero = false;
+      // P^T operands: k-step s2 covers keys 16*s2 .. +15 of the tile; lane
+      // element t is key 16*s2 + 8*(t>>2) + 4*hh + (t&3).
       bf16x8 pk[4];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -271,23 +341,25 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
         pk[2][e] = static_cast<__bf16>(s1[e]);
         pk[3][e] = static_cast<__bf16>(s1[8 + e]);
       }
-      // O^T += V^T P^T; V^T operand rows come from transposing LDS reads of
-      // the same permuted keys: rows 16*s2 + 4*hh + {0..3} and +8.
+      // O^T += V^T P^T; the V^T operand is two transposing reads of the same
+      // permuted keys (rows 16*s2 + 4*hh + {0..3} and +8).
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
+        const int r0 = 16 * s2 + vrow;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          const char* a = vb + v_off + 16 * s2 * kRowBytes + 64 * d;
+          const char* a = vb + r0 * kRowBytes + ((((4 * d + cq) ^ vsw0)) << 4) + 8 * (i16 & 1);
+          const char* a2 =
+              vb + (r0 + 8) * kRowBytes + ((((4 * d + cq) ^ vsw1)) << 4) + 8 * (i16 & 1);
           const i16x4 lo = lds_tr16(a);
-          const i16x4 hi = lds_tr16(a + 8 * kRowBytes);
-          const i16x8 cat = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, cat), pk[s2],
-                                                          o[d], 0, 0, 0);
+          const i16x4 hi = lds_tr16(a2);
+          const bf16x8 av =
+              __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pk[s2], o[d], 0, 0, 0);
         }
       }
     }
-    if (more) lstore(stage ^ 1);
-    __syncthreads();
+    stage = stage == kStages - 1 ? 0 : stage + 1;
   }
 
   // ---- epilogue: normalise, scatter O rows and log2-LSE ---------------------
@@ -333,10 +405,10 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
     return invalid("swattn_prefill_fwd: bad index counts");
   const int64_t total_q = static_cast<int64_t>(batch) * seq_q;
   const int64_t total_kv = static_cast<int64_t>(batch) * seq_kv;
-  if (total_q > INT32_MAX || total_kv > INT32_MAX)
+  if (total_q > INT32_MAX || total_kv > INT32_MAX - 2 * kBN)
     return invalid("swattn_prefill_fwd: batch*seq must stay below 2^31");
   const int group = heads_q / heads_kv;
-  if ((n_full + n_local) * static_cast<int64_t>(group) > INT32_MAX)
+  if ((n_full + n_local) * static_cast<int64_t>(group) > INT32_MAX - kRowsPerItem)
     return invalid("swattn_prefill_fwd: too many rows");
   const bool meta = full_starts != nullptr || local_starts != nullptr || causal_ends != nullptr;
   if (meta && (full_starts == nullptr || local_starts == nullptr || causal_ends == nullptr))
