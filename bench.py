@@ -103,12 +103,14 @@ def main():
     out = torch.empty_like(q)
     lse = torch.empty(q.shape[:3], dtype=torch.float32, device=dev)
     stream = _lib.stream_handle(dev)
+    ws_bytes_fwd = int(L.swattn_prefill_workspace_bytes(B, S, HKV, D))
+    ws_fwd = torch.empty(ws_bytes_fwd, dtype=torch.uint8, device=dev)
 
     def attn(fi, li):
         st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), fi.data_ptr(),
                                   fi.numel(), li.data_ptr(), li.numel(), None, None, None,
                                   out.data_ptr(), lse.data_ptr(), B, S, S, HQ, HKV, D, W, scale,
-                                  stream)
+                                  ws_fwd.data_ptr(), ws_bytes_fwd, stream)
         if st != 0:
             raise RuntimeError(L.swattn_last_error().decode())
 

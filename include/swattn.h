@@ -94,6 +94,14 @@ int swattn_build_metadata(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens
                           int32_t* causal_ends, void* stream);
 
 /*
+ * Workspace bytes swattn_prefill_fwd needs for K/V of this shape (V is
+ * repacked there as MFMA-ready V^T tiles); 0 for an unsupported shape.
+ * No counterpart in the reference: its TileLang kernel reads V in place.
+ */
+size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t heads_kv,
+                                      int32_t head_dim);
+
+/*
  * Routed GQA prefill forward, both branches in one launch.  Replaces the two
  * _switch_gqa_prefill_branch launches of switch_gqa_prefill_forward
  * (V:402-445; kernel body V:103-249, fixed-length rule F:69-214).
@@ -111,6 +119,8 @@ int swattn_build_metadata(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens
  *        lse uses the log2 convention: log2(sum_j 2^(s_j*c)) with
  *        c = scale_log2 and s_j the raw q.k products (V:236-241).
  *   scale_log2  softmax scale already multiplied by log2(e) (V:73-76).
+ *   workspace   device scratch of at least swattn_prefill_workspace_bytes();
+ *               overwritten by the call (calls sharing it must not overlap).
  */
 int swattn_prefill_fwd(const void* q, const void* k, const void* v,
                        const int32_t* full_idx, int64_t n_full,
@@ -119,7 +129,7 @@ int swattn_prefill_fwd(const void* q, const void* k, const void* v,
                        const int32_t* causal_ends, void* out, float* lse,
                        int32_t batch, int64_t seq_q, int64_t seq_kv, int32_t heads_q,
                        int32_t heads_kv, int32_t head_dim, int32_t window, float scale_log2,
-                       void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

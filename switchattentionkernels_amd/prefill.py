@@ -223,15 +223,19 @@ def switch_gqa_prefill_forward(
     assert threads == 128, "the qualified schedule uses 128 threads"
     scale = ((1.0 / dim) ** 0.5 if sm_scale is None else float(sm_scale)) * LOG2E
     md = metadata
+    L = _lib.lib()
+    ws_bytes = int(L.swattn_prefill_workspace_bytes(batch, kv_len, kv_heads, dim))
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
-        st = _lib.lib().swattn_prefill_fwd(
+        st = L.swattn_prefill_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(),
             full.data_ptr(), full.numel(), local.data_ptr(), local.numel(),
             _lib.ptr(md.full_starts) if md is not None else None,
             _lib.ptr(md.local_starts) if md is not None else None,
             _lib.ptr(md.causal_ends) if md is not None else None,
             output.data_ptr(), lse.data_ptr(), batch, q_len, kv_len, heads, kv_heads, dim,
-            int(window_size), scale, _lib.stream_handle(q.device))
+            int(window_size), scale, workspace.data_ptr(), ws_bytes,
+            _lib.stream_handle(q.device))
     _lib.check(st, "swattn_prefill_fwd")
     return output, lse
 

@@ -34,7 +34,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     funcs = _header_functions()
-    assert len(funcs) == 7, funcs
+    assert len(funcs) == 8, funcs
     lib = _lib.lib()
     for name in funcs:
         assert hasattr(lib, name), name
@@ -49,26 +49,29 @@ def test_version_and_workspace():
     assert lib.swattn_compact_workspace_bytes(16384) == 0
     assert lib.swattn_compact_workspace_bytes(16385) == 2 * 4
     assert lib.swattn_compact_workspace_bytes(65536) == 4 * 4
+    # V^T tiles: Hkv x ceil(B*Skv / 64) x 16 KiB
+    assert lib.swattn_prefill_workspace_bytes(2, 100, 8, 128) == 8 * 4 * 16384
+    assert lib.swattn_prefill_workspace_bytes(1, 100, 8, 64) == 0
 
 
 def test_host_side_argument_errors():
     lib = _lib.lib()
     # head_dim != 128
     st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, None, None, None, None, None,
-                                1, 1, 1, 1, 1, 64, 4, ctypes.c_float(1.0), None)
+                                1, 1, 1, 1, 1, 64, 4, ctypes.c_float(1.0), None, 0, None)
     assert st == -1 and b"head_dim" in lib.swattn_last_error()
     # heads_q not a multiple of heads_kv
     st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, None, None, None, None, None,
-                                1, 1, 1, 6, 4, 128, 4, ctypes.c_float(1.0), None)
+                                1, 1, 1, 6, 4, 128, 4, ctypes.c_float(1.0), None, 0, None)
     assert st == -1 and b"multiple" in lib.swattn_last_error()
     # partial metadata
     dummy = ctypes.c_void_p(16)
     st = lib.swattn_prefill_fwd(None, None, None, None, 1, None, 0, dummy, None, None, None, None,
-                                1, 1, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None)
+                                1, 1, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None, 0, None)
     assert st == -1 and b"metadata" in lib.swattn_last_error()
     # nothing to do is fine without touching the device
     st = lib.swattn_prefill_fwd(None, None, None, None, 0, None, 0, None, None, None, None, None,
-                                1, 0, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None)
+                                1, 0, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None, 0, None)
     assert st == 0
     assert lib.swattn_compact(None, -1, None, None, None, 0, None) == -1
     assert lib.swattn_check_indices(None, -1, None, 0, 5, None, None) == -1

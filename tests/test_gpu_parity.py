@@ -362,11 +362,13 @@ def test_c_abi_writes_only_listed_rows():
     out = torch.full_like(q, 7.0)
     lse = torch.full(q.shape[:3], -3.0, device=DEV)
     L = _lib.lib()
+    ws_bytes = L.swattn_prefill_workspace_bytes(1, 300, 2, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
     st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(),
                               full.numel(), None, 0, None, None, None, out.data_ptr(),
                               lse.data_ptr(), 1, 300, 300, 8, 2, 128, 64,
-                              ctypes.c_float(128 ** -0.5 * oracle.LOG2E),
-                              _lib.stream_handle(q.device))
+                              ctypes.c_float(128 ** -0.5 * oracle.LOG2E), ws.data_ptr(),
+                              ws_bytes, _lib.stream_handle(q.device))
     assert st == 0
     torch.cuda.synchronize()
     lm = ~m
