@@ -53,6 +53,9 @@ def parse():
     ap.add_argument("--no-sdpa", action="store_true", help="skip the torch SDPA comparator")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only loop the attention kernel (for rocprofv3 runs)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="with --kernel-only: also run 3 device copies of this many MiB "
+                         "(calibrates the HBM byte counters)")
     return ap.parse_args()
 
 
@@ -115,10 +118,24 @@ def main():
             raise RuntimeError(L.swattn_last_error().decode())
 
     if args.kernel_only:
-        for _ in range(args.warmup + args.steps):
-            attn(full, local)
-        torch.cuda.synchronize()
-        print(json.dumps({"kernel_only": True, "launches": args.warmup + args.steps}))
+        # The same entry-point launches the roofline figure times, so that a
+        # profiler's per-kernel averages over this run can be set beside it.
+        kernel_ms = time_launches(lambda: attn(full, local), args.steps, warmup=args.warmup)
+        # Calibration for HBM byte counters: a plain device-to-device copy of
+        # a known size (its FETCH_SIZE / WRITE_SIZE per dispatch, divided by
+        # these bytes, is the counter's scale factor).
+        calib = None
+        if args.calib_copy_mib > 0:
+            n = args.calib_copy_mib << 20
+            src = torch.ones(n, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            calib = {"copy_bytes_read": n, "copy_bytes_written": n, "copies": 3}
+        print(json.dumps({"kernel_only": True, "launches": args.warmup + args.steps,
+                          "timed_launches": args.steps, "entry_point_ms": round(kernel_ms, 4),
+                          "calibration": calib}))
         return
 
     # ---- timed region: K full steps -------------------------------------------
@@ -133,11 +150,11 @@ def main():
     print(f"[bench] {args.steps} steps, {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     # ---- attention kernel alone (roofline) -------------------------------------
-    attn_ms = time_launches(lambda: attn(full, local), max(args.steps, 10))
+    attn_ms = time_launches(lambda: attn(full, local), max(args.steps, 50), warmup=10)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
     ones = torch.ones_like(mask)
     f_all, l_all = build_switch_query_indices(ones)
-    dense_ms = time_launches(lambda: attn(f_all, l_all), max(args.steps // 2, 5))
+    dense_ms = time_launches(lambda: attn(f_all, l_all), max(args.steps, 20), warmup=5)
     ws_bytes = int(L.swattn_compact_workspace_bytes(S * B))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     idx = torch.empty(S * B, dtype=torch.int32, device=dev)
@@ -233,7 +250,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "fwd_kernel<false> (swattn_prefill_fwd)",
+                     "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false>",
                      "kernel_ms": round(attn_ms, 4)},
         "cpu_baseline": cpu,
         "comparators": {
