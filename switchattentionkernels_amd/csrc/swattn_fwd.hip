@@ -66,7 +66,7 @@ constexpr int kBN = 64;                               // keys per K/V tile
 constexpr int kWaves = 4;                             // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWave = 32;                      // one 32-row MFMA block
-constexpr int kRowsPerItem = kWaves * kRowsPerWave;   // 256 rows per work item
+constexpr int kRowsPerItem = kWaves * kRowsPerWave;   // 128 rows per work item
 constexpr int kRowBytes = kD * 2;                     // 256-byte K rows, unpadded
 constexpr int kVtRowBytes = kBN * 2;                  // 128-byte V^T rows (one d, 64 keys)
 constexpr int kTileBytes = kBN * kRowBytes;           // one K or V^T tile: 16 KiB
