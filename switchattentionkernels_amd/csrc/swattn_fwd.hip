@@ -14,7 +14,7 @@
 // * Work item = (branch, tile of 128 "rows", KV head).  A row is a
 //   (compacted query slot, query head of the KV head's group) pair with the
 //   head index fastest, so one K/V tile in LDS serves every query head of the
-//   group (GQA packing) and a wave's rows span only 64/G query positions.
+//   group (GQA packing) and a wave's 32 rows span only 32/G query positions.
 // * The whole routed problem is one grid: full-branch tiles first, last tile
 //   (longest causal prefix) first, then local tiles; KV head = item % Hkv so
 //   that with Hkv = 8 every XCD (blockIdx % 8) streams a single KV head
@@ -35,14 +35,21 @@
 //   (a transposing LDS read of row-major V measured under half that rate).
 //   The pre-pass moves 2 x |V| bytes through HBM, a few percent of the
 //   attention time.
-// * K/V tiles stream global -> LDS with global_load_lds_dwordx4 (no register
-//   staging) through a ring of LDS stages, one tile ahead of the compute, with
-//   one barrier per tile.  The loads are issued from inline assembly and
+// * K/V^T tiles stream global -> LDS with buffer_load_dwordx4 ... lds (no
+//   register staging) into a two-slot K ring and a two-slot V^T ring, with
+//   one barrier per tile.  The buffer descriptor's range check stops a tile
+//   at the end of the sequence, so there is no clamped slow path and no
+//   branch around the loads.  The loads are issued from inline assembly and
 //   waited for with explicit vmcnt counts: the compiler cannot see that they
-//   target another stage than the one being read, and would otherwise drain
+//   target another slot than the one being read, and would otherwise drain
 //   every load before each LDS read.  LDS rows are unpadded 256-byte rows
 //   whose 16-byte chunks are XOR-swizzled so both operand read patterns are
 //   conflict-free.
+// * The tile loop is software-pipelined inside each wave: while the matrix
+//   cores compute S for tile j+1, the VALU turns S(j) into P(j); while they
+//   accumulate P(j) V(j), the VALU sums P(j) and takes the max of S(j+1).
+//   K therefore runs one tile ahead of V^T.  Each phase is one basic block
+//   with an explicit MFMA/VALU/LDS-read interleave.
 // * The running max is only moved when it grows by more than 2^8 in the
 //   exp2 domain (rescaling O is then rare); P = 2^(s*c - m*c) stays below
 //   2^8, and O = acc / l, LSE = log2(l) + m*c are the same quantities as with
@@ -71,11 +78,15 @@ constexpr int kRowBytes = kD * 2;                     // 256-byte K rows, unpadd
 constexpr int kVtRowBytes = kBN * 2;                  // 128-byte V^T rows (one d, 64 keys)
 constexpr int kTileBytes = kBN * kRowBytes;           // one K or V^T tile: 16 KiB
 static_assert(kD * kVtRowBytes == kTileBytes, "K and V^T tiles have the same size");
-constexpr int kStageBytes = 2 * kTileBytes;           // K + V
-constexpr int kStages = 2;                            // LDS ring depth
-constexpr int kLdsBytes = kStages * kStageBytes;      // 64 KiB: two workgroups per CU
+// LDS: a two-slot K ring followed by a two-slot V^T ring (K runs one tile
+// ahead of V^T).  64 KiB: two workgroups per CU.
+constexpr int kVRing = 2 * kTileBytes;                // byte offset of the V^T ring
+constexpr int kLdsBytes = 4 * kTileBytes;
 constexpr int kRowsPerLoader = kBN / kWaves;          // key rows each wave stages per tile
 static_assert(kRowsPerLoader % 4 == 0, "a wave stages whole 1 KiB blocks of K and V^T");
+// s_waitcnt immediate (gfx9 layout) for vmcnt(0) with expcnt and lgkmcnt
+// left unconstrained: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
 constexpr float kMaxSentinel = -1073741824.0f;        // -2^30 (V:174)
 
 struct FwdParams {
@@ -132,22 +143,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
 }
-// 16 bytes per lane from global memory to LDS at lds_base + 16 * lane
-// (global_load_lds_dwordx4; the LDS base goes through M0 and must be
-// wave-uniform).  Issued as inline assembly so that the compiler's wait
-// insertion does not treat it as a store that aliases every LDS read.
-// dma16 takes a per-lane 64-bit address; dma16_sbase a wave-uniform base in
-// SGPRs plus a per-lane 32-bit byte offset (no per-tile address arithmetic).
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(lds_base)
-               : "memory", "m0");
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records
+// bytes, 32-bit data format.  Lanes whose offset is >= num_records read
+// nothing, so one descriptor covers a tile that is cut short by the end of
+// the sequence, and num_records = 0 turns every load off.
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(a >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  r[3] = kRsrcWord3;
+  return r;
 }
-__device__ __forceinline__ void dma16_sbase(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+
+// 16 bytes per lane from buffer offset voff to LDS at lds_base + 16 * lane
+// (buffer_load_dwordx4 ... lds; the LDS base goes through M0 and must be
+// wave-uniform).  Issued as inline assembly so that the compiler's wait
+// insertion does not treat it as a store that aliases every LDS read; the
+// memory clobber keeps it in order with the LDS reads around it.
+__device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
-               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "v"(voff), "s"(rsrc), "s"(lds_base)
                : "memory", "m0");
 }
 __device__ __forceinline__ uint32_t lds_addr(const char* p) {
@@ -166,8 +187,6 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 struct StagePlan {
   uint32_t koff[kRowsPerLoader / 4];   // byte offset of this lane's K chunk from the tile's first key
   uint32_t voff[kRowsPerLoader / 4];   // byte offset of this lane's V^T chunk inside the V^T tile
-  int krow[kRowsPerLoader / 4];        // key row inside the tile (for the clamped last tile)
-  int kchunk[kRowsPerLoader / 4];
   uint32_t lds_w;                      // this wave's byte offset inside a K (or V^T) tile
 };
 
@@ -178,8 +197,6 @@ __device__ __forceinline__ StagePlan make_stage_plan(const FwdParams& p, int kvh
   for (int i = 0; i < kRowsPerLoader / 4; ++i) {
     const int row = kRowsPerLoader * wave + 4 * i + (lane >> 4);
     const int j = (lane & 15) ^ swz(row);
-    sp.krow[i] = row;
-    sp.kchunk[i] = j;
     sp.koff[i] = static_cast<uint32_t>(((row * p.hkv + kvh) * kD + 8 * j) * 2);
     const int d = 2 * kRowsPerLoader * wave + 8 * i + (lane >> 3);
     const int jv = (lane & 7) ^ vswz(d);
@@ -189,32 +206,32 @@ __device__ __forceinline__ StagePlan make_stage_plan(const FwdParams& p, int kvh
   return sp;
 }
 
-// Issue the loads of tile tk into the stage at LDS byte address stage_lds
-// (kLoadsPerTile loads per lane).
-__device__ __forceinline__ void stage_tile(const FwdParams& p, const StagePlan& sp,
-                                           uint32_t stage_lds, int tk, int kvh) {
-  const char* vt_tile = reinterpret_cast<const char*>(p.vt) +
-                        (static_cast<int64_t>(kvh) * p.kv_tiles + tk) * kTileBytes;
-  const uint32_t lbase = __builtin_amdgcn_readfirstlane(stage_lds + sp.lds_w);
-  if ((tk + 1) * kBN <= p.total_kv) {
-    const char* k_tile = reinterpret_cast<const char*>(p.k) +
-                         static_cast<int64_t>(tk) * kBN * p.hkv * kD * 2;
-#pragma unroll
-    for (int i = 0; i < kRowsPerLoader / 4; ++i) {
-      dma16_sbase(k_tile, sp.koff[i], lbase + 4 * i * kRowBytes);
-      dma16_sbase(vt_tile, sp.voff[i], lbase + 4 * i * kRowBytes + kTileBytes);
-    }
-  } else {
-    // Last, partial tile: clamp the key so that every lane reads inside K
-    // (the rows past total_kv are masked out of every row's range).
-#pragma unroll
-    for (int i = 0; i < kRowsPerLoader / 4; ++i) {
-      const int key = min(tk * kBN + sp.krow[i], p.total_kv - 1);
-      dma16(p.k + (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 8 * sp.kchunk[i],
-            lbase + 4 * i * kRowBytes);
-      dma16_sbase(vt_tile, sp.voff[i], lbase + 4 * i * kRowBytes + kTileBytes);
-    }
-  }
+// Buffer descriptor for K tile tk of KV head kvh (any lane offset of the
+// staging plan); rows past total_kv fall outside it.  `live` = false gives an
+// empty descriptor: the step's K loads then move nothing.
+__device__ __forceinline__ i32x4 k_rsrc(const FwdParams& p, int tk, bool live) {
+  const int64_t row_bytes = static_cast<int64_t>(p.hkv) * kD * 2;
+  const int t = live ? tk : 0;
+  const int64_t rest = (static_cast<int64_t>(p.total_kv) - static_cast<int64_t>(t) * kBN) * row_bytes;
+  const uint32_t n = live ? static_cast<uint32_t>(rest < 0xffffffffLL ? rest : 0xffffffffLL) : 0u;
+  return make_rsrc(reinterpret_cast<const char*>(p.k) + static_cast<int64_t>(t) * kBN * row_bytes, n);
+}
+
+// Buffer descriptor for V^T tile tk of KV head kvh (zero-padded, always whole).
+__device__ __forceinline__ i32x4 v_rsrc(const FwdParams& p, int tk, int kvh, bool live) {
+  const int t = live ? tk : 0;
+  return make_rsrc(reinterpret_cast<const char*>(p.vt) +
+                       (static_cast<int64_t>(kvh) * p.kv_tiles + t) * kTileBytes,
+                   live ? static_cast<uint32_t>(kTileBytes) : 0u);
+}
+
+// Load i (of kRowsPerLoader / 4) of this wave's share of a K or V^T tile
+// into the slot at LDS byte address slot.
+__device__ __forceinline__ void stage_k(const StagePlan& sp, const i32x4& rs, uint32_t slot, int i) {
+  dma16(rs, sp.koff[i], __builtin_amdgcn_readfirstlane(slot + sp.lds_w + 4 * i * kRowBytes));
+}
+__device__ __forceinline__ void stage_v(const StagePlan& sp, const i32x4& rs, uint32_t slot, int i) {
+  dma16(rs, sp.voff[i], __builtin_amdgcn_readfirstlane(slot + sp.lds_w + 4 * i * kRowBytes));
 }
 
 // V [total_kv, Hkv, 128] -> V^T tiles [Hkv][kv_tiles][128][64]: row d of tile
@@ -290,97 +307,92 @@ __device__ __forceinline__ void mask_tile(f32x16& s0, f32x16& s1, int lo, int hi
   }
 }
 
-// Online-softmax step of one 32-row x 64-key tile held as two S^T blocks.
-// The max m only moves when the tile max exceeds it by more than 8 in the
-// exp2 domain (or m is still the sentinel); alpha is then the O rescale
-// factor, otherwise exactly 1.  Overwrites s0/s1 with P = 2^(s*c - m*c)
-// (fp32) and returns whether m moved.
-__device__ __forceinline__ bool softmax_step(f32x16& s0, f32x16& s1, float& m, float& l, float c,
-                                             float& alpha) {
-  // 32 values -> 16 three-input maxima.
+// Row max of a 32-row x 64-key tile held as two S^T blocks: 32 values per
+// lane in 16 three-input maxima, then the other half-wave's 32 keys.
+__device__ __forceinline__ float tile_max(const f32x16& s0, const f32x16& s1) {
   float mx = fmaxf(fmaxf(s0[0], s0[1]), s0[2]);
 #pragma unroll
   for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, s0[e]), s0[e + 1]);
   mx = fmaxf(fmaxf(mx, s0[15]), s1[0]);
 #pragma unroll
   for (int e = 1; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s1[e]), s1[e + 1 < 16 ? e + 1 : e]);
-  mx = xor32_max(mx);
-  const bool moved = (mx - m) * c > 8.0f;
-  const float m_new = moved ? mx : m;
-  alpha = moved ? __builtin_amdgcn_exp2f((m - m_new) * c) : 1.0f;
-  const float mc = m_new * c;
-  float rs0 = 0.f, rs1 = 0.f;
+  return xor32_max(mx);
+}
+
+// P = 2^(s*c - m*c) in place.
+__device__ __forceinline__ void tile_exp(f32x16& s0, f32x16& s1, float c, float mc) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     s0[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[e], c, -mc));
     s1[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[e], c, -mc));
-    rs0 += s0[e];
-    rs1 += s1[e];
   }
-  const float rs = xor32_sum(rs0 + rs1);
-  l = l * alpha + rs;
-  m = m_new;
-  return moved;
+}
+
+// Row sum of the fp32 P tile (both half-waves).
+__device__ __forceinline__ float tile_sum(const f32x16& s0, const f32x16& s1) {
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    a += s0[e];
+    b += s1[e];
+  }
+  return xor32_sum(a + b);
 }
 
 // Per-wave loop state and per-lane constants.
 struct WaveCtx {
   bf16x8 qf[8];        // Q^T B operands
-  int koff[8];         // K operand LDS offsets (stage-relative), k-step kk
-  int voff[4];         // V^T operand LDS offsets (stage-relative), k-step s2
+  int koff[8];         // K operand LDS offsets (slot-relative), k-step kk
+  int voff[4];         // V^T operand LDS offsets (slot-relative), k-step s2
   int ks, ke;          // this lane's row range
   int w_min_s, w_max_e, w_max_s, w_min_e;
   int hh;
   float c;
   f32x16 o[4];
   float m, l;
+  float alpha;         // O / l rescale factor of the last tile whose max was taken
+  bool rescale;        // some lane's max moved at that tile
   bool o_zero;
 };
 
-// One 64-key tile read from LDS stage kStage (compile-time, so every LDS
-// address is a per-lane register plus an immediate).
-template <int kStage>
-__device__ __forceinline__ void tile_step(const FwdParams& p, const StagePlan& sp, char* smem,
-                                          int tk, int t_end, int kvh, WaveCtx& w) {
-  static_assert(kStages == 2, "tile_step assumes a two-stage ring");
-  // This lane's loads of tile tk are complete; after the barrier everyone's
-  // are, and every wave has finished reading the other stage, which the
-  // loads issued next overwrite.
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (tk + 1 < t_end) stage_tile(p, sp, lds_addr(smem) + (kStage ^ 1) * kStageBytes, tk + 1, kvh);
+__device__ __forceinline__ bool wave_has_keys(const WaveCtx& w, int tk) {
   const int key0 = tk * kBN;
-  if (key0 >= w.w_max_e || key0 + kBN <= w.w_min_s) return;  // no row of this wave
-  const char* kb = smem + kStage * kStageBytes;
-  const char* vb = kb + kTileBytes;
-  // S^T = K Q^T: two 32-key blocks.
-  f32x16 s0 = f32x16{}, s1 = f32x16{};
+  return key0 < w.w_max_e && key0 + kBN > w.w_min_s;
+}
+
+// S^T = K Q^T for the K tile at kb: two 32-key blocks, one 16-byte K read per
+// MFMA.  The step's K staging loads (into another slot) are spread over the
+// tile, one after every second pair of reads.
+__device__ __forceinline__ void qk_tile(const char* kb, const WaveCtx& w, f32x16& s0, f32x16& s1,
+                                        const StagePlan& sp, const i32x4& krs, uint32_t kslot) {
+  s0 = f32x16{};
+  s1 = f32x16{};
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) {
     const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kb + w.koff[kk]);
     const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kb + w.koff[kk] + 32 * kRowBytes);
+    if (kk & 1) stage_k(sp, krs, kslot, kk >> 1);
     s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, w.qf[kk], s0, 0, 0, 0);
     s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, w.qf[kk], s1, 0, 0, 0);
   }
-  if (!(key0 >= w.w_max_s && key0 + kBN <= w.w_min_e))
-    mask_tile(s0, s1, w.ks - key0 - 4 * w.hh, w.ke - key0 - 4 * w.hh);
-  float alpha;
-  const bool moved = softmax_step(s0, s1, w.m, w.l, w.c, alpha);
-  if (!w.o_zero && wave_ballot(moved)) {
-#pragma unroll
-    for (int d = 0; d < 4; ++d) w.o[d] *= alpha;
-  }
-  w.o_zero = false;
-  // P^T operands: k-step s2 covers keys 16*s2 .. +15 of the tile; lane
-  // element t is key 16*s2 + 8*(t>>2) + 4*hh + (t&3).
-  bf16x8 pk[4];
+}
+
+// P^T as bf16 MFMA B operands: k-step s2 covers keys 16*s2 .. +15 of the
+// tile; lane element t is key 16*s2 + 8*(t>>2) + 4*hh + (t&3).
+__device__ __forceinline__ void pack_p(const f32x16& p0, const f32x16& p1, bf16x8 (&pk)[4]) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    pk[0][e] = static_cast<__bf16>(s0[e]);
-    pk[1][e] = static_cast<__bf16>(s0[8 + e]);
-    pk[2][e] = static_cast<__bf16>(s1[e]);
-    pk[3][e] = static_cast<__bf16>(s1[8 + e]);
+    pk[0][e] = static_cast<__bf16>(p0[e]);
+    pk[1][e] = static_cast<__bf16>(p0[8 + e]);
+    pk[2][e] = static_cast<__bf16>(p1[e]);
+    pk[3][e] = static_cast<__bf16>(p1[8 + e]);
   }
-  // O^T += V^T P^T, one 16-byte V^T read per MFMA.
+}
+
+// O^T += V^T P^T for the V^T tile at vb, one 16-byte V^T read per MFMA; the
+// step's V^T staging loads are spread over the tile, one per k-step.
+__device__ __forceinline__ void pv_tile(const char* vb, WaveCtx& w, const bf16x8 (&pk)[4],
+                                        const StagePlan& sp, const i32x4& vrs, uint32_t vslot) {
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
@@ -388,7 +400,126 @@ __device__ __forceinline__ void tile_step(const FwdParams& p, const StagePlan& s
       const bf16x8 av = *reinterpret_cast<const bf16x8*>(vb + w.voff[s2] + 32 * d * kVtRowBytes);
       w.o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pk[s2], w.o[d], 0, 0, 0);
     }
+    stage_v(sp, vrs, vslot, s2);
   }
+}
+
+// Take the max of the (masked) S tile n0/n1 into the running max.  m only
+// moves when the tile max exceeds it by more than 8 in the exp2 domain (or m
+// is still the sentinel); alpha is then the rescale factor for O and l,
+// otherwise exactly 1.
+__device__ __forceinline__ void take_max(const f32x16& n0, const f32x16& n1, WaveCtx& w) {
+  const float mx = tile_max(n0, n1);
+  const bool moved = (mx - w.m) * w.c > 8.0f;
+  const float m_new = moved ? mx : w.m;
+  w.alpha = moved ? __builtin_amdgcn_exp2f((w.m - m_new) * w.c) : 1.0f;
+  w.rescale = wave_ballot(moved) != 0;
+  w.m = m_new;
+}
+
+// Scheduling pattern for a region holding 16 MFMAs, their 16 LDS operand
+// reads and independent VALU work: two reads up front, then each MFMA is
+// followed by kValu VALU instructions and the next read.  Instruction masks:
+// 0x008 MFMA, 0x002 VALU, 0x100 LDS read.
+template <int kValu>
+__device__ __forceinline__ void interleave_16_mfma() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+}
+
+// One pipeline step, for tile j = t_begin + r:
+//   phase A: S(j+1) = K(j+1) Q^T on the matrix cores while the VALU turns
+//            S(j) into P(j) (m, taken in the previous step, is final for j);
+//   between: the (rare) O rescale for tile j and the mask of S(j+1);
+//   phase B: O += V(j) P(j) on the matrix cores while the VALU sums P(j)
+//            and takes the max of S(j+1).
+// The two phases are single basic blocks, so the compiler interleaves the
+// independent MFMA and VALU streams.  kPar = r & 1 selects the LDS slots
+// (K read kPar^1, V^T read kPar) and the S buffers (current sb[kPar], next
+// sb[kPar^1]) at compile time.  Every wave stages its share of K(j+2) into
+// K slot kPar during phase A and of V^T(j+1) into V^T slot kPar^1 during
+// phase B, whatever it computes itself.
+template <int kPar, bool kS, bool kPV>
+__device__ __forceinline__ void pipe_body(const char* smem, const StagePlan& sp, const i32x4& krs,
+                                          const i32x4& vrs, int j, WaveCtx& w,
+                                          f32x16 (&sb)[2][2]) {
+  const char* kb = smem + (kPar ^ 1) * kTileBytes;
+  const char* vb = smem + kVRing + kPar * kTileBytes;
+  const uint32_t lds0 = lds_addr(smem);
+  const uint32_t kslot = lds0 + kPar * kTileBytes;
+  const uint32_t vslot = lds0 + kVRing + (kPar ^ 1) * kTileBytes;
+  f32x16& c0 = sb[kPar][0];
+  f32x16& c1 = sb[kPar][1];
+  f32x16& n0 = sb[kPar ^ 1][0];
+  f32x16& n1 = sb[kPar ^ 1][1];
+  // phase A
+  bf16x8 pk[4];
+  if constexpr (kS) {
+    qk_tile(kb, w, n0, n1, sp, krs, kslot);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLoader / 4; ++i) stage_k(sp, krs, kslot, i);
+  }
+  if constexpr (kPV) {
+    tile_exp(c0, c1, w.c, w.m * w.c);
+    pack_p(c0, c1, pk);
+    if constexpr (kS) interleave_16_mfma<5>();   // 32 fma + 32 exp + 16 cvt
+    // Materialise P here: without this the compiler sinks the exponentials
+    // past the branches below into phase B, next to their only MFMA users,
+    // and phase A is left with no VALU work to hide under its MFMAs.
+    asm volatile("" : "+v"(c0), "+v"(c1), "+v"(pk[0]), "+v"(pk[1]), "+v"(pk[2]), "+v"(pk[3]));
+  }
+  // between the phases
+  if constexpr (kPV) {
+    if (w.rescale && !w.o_zero) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) w.o[d] *= w.alpha;
+    }
+    w.o_zero = false;
+  }
+  if constexpr (kS) {
+    const int key0 = (j + 1) * kBN;
+    if (!(key0 >= w.w_max_s && key0 + kBN <= w.w_min_e))
+      mask_tile(n0, n1, w.ks - key0 - 4 * w.hh, w.ke - key0 - 4 * w.hh);
+  }
+  // phase B
+  if constexpr (kPV) {
+    pv_tile(vb, w, pk, sp, vrs, vslot);
+    w.l = w.l * w.alpha + tile_sum(c0, c1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRowsPerLoader / 4; ++i) stage_v(sp, vrs, vslot, i);
+  }
+  if constexpr (kS) take_max(n0, n1, w);
+  if constexpr (kS && kPV) interleave_16_mfma<4>();   // row sum + row max, ~65 VALU
+}
+
+template <int kPar>
+__device__ __forceinline__ void pipe_step(const FwdParams& p, const StagePlan& sp, char* smem,
+                                          int r, int t_begin, int n_tiles, int kvh, WaveCtx& w,
+                                          f32x16 (&sb)[2][2]) {
+  // Every lane's loads of K(j+1) and V(j) are complete after the barrier, and
+  // every wave has finished step r-1, which read the K slot and the V^T slot
+  // that this step's loads overwrite.
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const int j = t_begin + r;
+  const i32x4 krs = k_rsrc(p, j + 2, r + 2 < n_tiles);
+  const i32x4 vrs = v_rsrc(p, j + 1, kvh, r + 1 < n_tiles);
+  const bool do_s = r + 1 < n_tiles && wave_has_keys(w, j + 1);
+  const bool do_pv = r >= 0 && wave_has_keys(w, j);
+  if (do_s && do_pv)
+    pipe_body<kPar, true, true>(smem, sp, krs, vrs, j, w, sb);
+  else if (do_s)
+    pipe_body<kPar, true, false>(smem, sp, krs, vrs, j, w, sb);
+  else if (do_pv)
+    pipe_body<kPar, false, true>(smem, sp, krs, vrs, j, w, sb);
+  else
+    pipe_body<kPar, false, false>(smem, sp, krs, vrs, j, w, sb);
 }
 
 template <bool kMeta>
@@ -447,7 +578,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) w.qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // Wait for the Q loads with the builtin, not inline assembly: the compiler
+  // then knows they are complete.  Otherwise it keeps them "outstanding"
+  // into the tile loop and, at their first use there, emits vmcnt waits that
+  // also drain the next tile's LDS loads issued by then.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
 
   // ---- per-lane LDS operand offsets (stage-relative) --------------------------
   // K operand (A of S^T): key row rl (+32 for the second block), logical
@@ -467,13 +602,23 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   for (int d = 0; d < 4; ++d) w.o[d] = f32x16{};
   w.m = kMaxSentinel;
   w.l = 0.f;
+  w.alpha = 1.f;
+  w.rescale = false;
   w.o_zero = true;  // O is still exactly zero: a rescale can be skipped
 
-  // ---- main loop: the two-stage ring, unrolled so the stage is static -------
-  if (t_begin < t_end) stage_tile(p, sp, lds_addr(smem), t_begin, kvh);
-  for (int tk = t_begin; tk < t_end; tk += 2) {
-    tile_step<0>(p, sp, smem, tk, t_end, kvh, w);
-    if (tk + 1 < t_end) tile_step<1>(p, sp, smem, tk + 1, t_end, kvh, w);
+  // ---- main loop: step r computes S(t_begin+r+1) and O += V P(t_begin+r) -----
+  // Unrolled by two so that LDS slots and S buffers are static; step -1 only
+  // computes the first S tile.
+  const int n_tiles = t_end - t_begin;
+  f32x16 sb[2][2];
+  {
+    const i32x4 krs = k_rsrc(p, t_begin, n_tiles > 0);
+#pragma unroll
+    for (int i = 0; i < kRowsPerLoader / 4; ++i) stage_k(sp, krs, lds_addr(smem), i);
+  }
+  for (int r = -1; r < n_tiles; r += 2) {
+    pipe_step<1>(p, sp, smem, r, t_begin, n_tiles, kvh, w, sb);
+    if (r + 1 < n_tiles) pipe_step<0>(p, sp, smem, r + 1, t_begin, n_tiles, kvh, w, sb);
   }
 
   // ---- epilogue: normalise, scatter O rows and log2-LSE ---------------------
