@@ -15,8 +15,9 @@
 //   (compacted query slot, query head of the KV head's group) pair with the
 //   head index fastest, so one K/V tile in LDS serves every query head of the
 //   group (GQA packing) and a wave's 32 rows span only 32/G query positions.
-// * The whole routed problem is one grid: full-branch tiles first, last tile
-//   (longest causal prefix) first, then local tiles; KV head = item % Hkv so
+// * The whole routed problem is one grid: full-branch tiles first, then
+//   local tiles, each branch from its last tile (latest positions) down, so
+//   that work items come roughly longest first; KV head = item % Hkv so
 //   that with Hkv = 8 every XCD (blockIdx % 8) streams a single KV head
 //   through its own L2.  Counts come from the index lists' lengths, so new
 //   routing never recompiles anything.
@@ -70,7 +71,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kD = 128;                               // head_dim
 constexpr int kBN = 64;                               // keys per K/V tile
-constexpr int kWaves = 4;                             // waves per workgroup
+#ifndef SWATTN_WAVES
+#define SWATTN_WAVES 4
+#endif
+constexpr int kWaves = SWATTN_WAVES;                  // waves per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kRowsPerWave = 32;                      // one 32-row MFMA block
 constexpr int kRowsPerItem = kWaves * kRowsPerWave;   // 128 rows per work item
@@ -84,6 +88,8 @@ constexpr int kVRing = 2 * kTileBytes;                // byte offset of the V^T 
 constexpr int kLdsBytes = 4 * kTileBytes;
 constexpr int kRowsPerLoader = kBN / kWaves;          // key rows each wave stages per tile
 static_assert(kRowsPerLoader % 4 == 0, "a wave stages whole 1 KiB blocks of K and V^T");
+constexpr int kLoads = kRowsPerLoader / 4;            // loads per lane per K (or V^T) tile
+static_assert(kLoads == 1 || kLoads == 2 || kLoads == 4, "loads spread over 8 / 4 k-steps");
 // s_waitcnt immediate (gfx9 layout) for vmcnt(0) with expcnt and lgkmcnt
 // left unconstrained: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
 constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xF << 8);
@@ -371,7 +377,7 @@ __device__ __forceinline__ void qk_tile(const char* kb, const WaveCtx& w, f32x16
   for (int kk = 0; kk < 8; ++kk) {
     const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kb + w.koff[kk]);
     const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kb + w.koff[kk] + 32 * kRowBytes);
-    if (kk & 1) stage_k(sp, krs, kslot, kk >> 1);
+    if ((kk + 1) % (8 / kLoads) == 0) stage_k(sp, krs, kslot, kk / (8 / kLoads));
     s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, w.qf[kk], s0, 0, 0, 0);
     s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, w.qf[kk], s1, 0, 0, 0);
   }
@@ -400,7 +406,7 @@ __device__ __forceinline__ void pv_tile(const char* vb, WaveCtx& w, const bf16x8
       const bf16x8 av = *reinterpret_cast<const bf16x8*>(vb + w.voff[s2] + 32 * d * kVtRowBytes);
       w.o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, pk[s2], w.o[d], 0, 0, 0);
     }
-    stage_v(sp, vrs, vslot, s2);
+    if ((s2 + 1) % (4 / kLoads) == 0) stage_v(sp, vrs, vslot, s2 / (4 / kLoads));
   }
 }
 
@@ -537,7 +543,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int kvh = item % p.hkv;
   const int t = item / p.hkv;
   const int branch = t < p.tiles[0] ? 0 : 1;
-  const int tile = branch == 0 ? p.tiles[0] - 1 - t : t - p.tiles[0];
+  // Both branches run their last tile (latest positions) first: full tiles
+  // are then ordered by falling causal length, and the local tiles that end
+  // the grid are the short ones whose window is cut at the sequence start.
+  const int tile = branch == 0 ? p.tiles[0] - 1 - t : p.tiles[0] + p.tiles[1] - 1 - t;
   const int32_t* __restrict__ idx = p.idx[branch];
   const int count = p.count[branch];
   const int G = p.group;
