@@ -107,8 +107,43 @@ def _raise_for(flags: int, which: str) -> None:
             raise ValueError(MSG_ORDER)
 
 
+class _Compaction:
+    """Identity of one ``build_switch_query_indices`` result (``n`` positions)."""
+
+    __slots__ = ("n",)
+
+    def __init__(self, n: int):
+        self.n = n
+
+
+def _tag_compacted(full: torch.Tensor, local: torch.Tensor, n: int) -> None:
+    """Mark a fresh compaction result.  Both lists are ascending, disjoint and
+    cover ``[0, n)`` by construction; torch's version counter (shared by the
+    two views of one buffer) shows whether either was modified since."""
+    token = _Compaction(n)
+    full._swattn_compaction = (token, "full", full._version)
+    local._swattn_compaction = (token, "local", local._version)
+
+
+def _is_untouched_compaction(full, local, seq_len: int) -> bool:
+    a = getattr(full, "_swattn_compaction", None)
+    b = getattr(local, "_swattn_compaction", None)
+    return (a is not None and b is not None and a[0] is b[0] and a[0].n == seq_len
+            and a[1] == "full" and b[1] == "local"
+            and full._version == a[2] and local._version == b[2])
+
+
 def _check_lists(full_query_indices, local_query_indices, seq_len: int, device):
-    """V:384-393 in the reference's order, plus disjointness last."""
+    """V:384-393 in the reference's order, plus disjointness last.
+
+    A pair returned by ``build_switch_query_indices`` for this sequence length
+    and not modified since is valid by construction: only the device check
+    runs for it, and the device-side scan and its blocking read are skipped.
+    """
+    if _is_untouched_compaction(full_query_indices, local_query_indices, seq_len):
+        if full_query_indices.device != device or local_query_indices.device != device:
+            raise ValueError("query indices must be on the same device as Q")
+        return full_query_indices, local_query_indices
     full = _prepare_indices(full_query_indices, device=device)
     try:
         local = _prepare_indices(local_query_indices, device=device)
@@ -170,7 +205,9 @@ def build_switch_query_indices(full_mask: torch.Tensor) -> Tuple[torch.Tensor, t
                               ws.data_ptr(), ws_bytes, _lib.stream_handle(dev))
     _lib.check(st, "swattn_compact")
     nf = int(counts[0].item())
-    return out[:nf], out[nf:]
+    full, local = out[:nf], out[nf:]
+    _tag_compacted(full, local, n)
+    return full, local
 
 
 def switch_gqa_prefill_forward(

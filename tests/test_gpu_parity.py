@@ -163,6 +163,40 @@ def test_index_validation_errors():
         build_switch_query_indices(torch.zeros(4, dtype=torch.int32, device=DEV))
 
 
+def test_compaction_output_skips_only_when_untouched():
+    """Lists straight from build_switch_query_indices skip the device scan;
+    anything else (modified in place, mixed pairs, swapped roles, another
+    length) is validated in full and raises the reference's errors."""
+    s = 64
+    q, k, v = (t.to(DEV) for t in _qkv(3, 1, s, 4, 2))
+    m = _mask(3, (s,), 0.5)
+    full, local = build_switch_query_indices(m.to(DEV))
+    o_ok, lse_ok = switch_gqa_prefill_forward(q, k, v, full, local, window_size=8)
+    # modified in place: order broken -> the scan runs again and raises
+    full2, local2 = build_switch_query_indices(m.to(DEV))
+    full2[0], full2[1] = full2[1].clone(), full2[0].clone()
+    with pytest.raises(ValueError, match=re.escape("query indices must be strictly increasing")):
+        switch_gqa_prefill_forward(q, k, v, full2, local2, window_size=8)
+    # a pair mixed from two compactions: validated (overlap / coverage)
+    fa, la = build_switch_query_indices(m.to(DEV))
+    fb, lb = build_switch_query_indices((~m).to(DEV))
+    exc, msg = R.first_error(fa.cpu().numpy(), lb.cpu().numpy(), s)
+    with pytest.raises(exc, match=re.escape(msg)):
+        switch_gqa_prefill_forward(q, k, v, fa, lb, window_size=8)
+    # swapped roles are valid lists with different routing: computed, not skipped
+    o_sw, lse_sw = switch_gqa_prefill_forward(q, k, v, local, full, window_size=8)
+    o_ref, lse_ref = oracle.routed_attention(q.cpu(), k.cpu(), v.cpu(), local.cpu().numpy(),
+                                             full.cpu().numpy(), window_size=8)
+    _assert_close(o_sw, lse_sw, o_ref, lse_ref, tag="swapped")
+    # compacted for another length: validated against this one and rejected
+    fs, ls = build_switch_query_indices(m[: s // 2].to(DEV))
+    with pytest.raises(ValueError, match=re.escape("full and local query lists must cover")):
+        switch_gqa_prefill_forward(q, k, v, fs, ls, window_size=8)
+    # the untouched pair gives the same result as the same lists without the tag
+    o_2, lse_2 = switch_gqa_prefill_forward(q, k, v, full.clone(), local.clone(), window_size=8)
+    assert torch.equal(o_ok, o_2) and torch.equal(lse_ok, lse_2)
+
+
 def test_metadata_validation_errors():
     q, k, v = (t.to(DEV) for t in _qkv(2, 1, 16, 4, 2))
     md = build_switch_attention_metadata(16, 16, device=q.device, window_size=4)
