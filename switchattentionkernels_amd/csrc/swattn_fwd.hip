@@ -352,6 +352,7 @@ struct WaveCtx {
   int voff[4];         // V^T operand LDS offsets (slot-relative), k-step s2
   int ks, ke;          // this lane's row range
   int w_min_s, w_max_e, w_max_s, w_min_e;
+  int it0, it1;        // tiles inside every row's range (no mask): [it0, it1)
   int hh;
   float c;
   f32x16 o[4];
@@ -489,9 +490,10 @@ __device__ __forceinline__ void pipe_body(const char* smem, const StagePlan& sp,
     w.o_zero = false;
   }
   if constexpr (kS) {
-    const int key0 = (j + 1) * kBN;
-    if (!(key0 >= w.w_max_s && key0 + kBN <= w.w_min_e))
+    if (j + 1 < w.it0 || j + 1 >= w.it1) {
+      const int key0 = (j + 1) * kBN;
       mask_tile(n0, n1, w.ks - key0 - 4 * w.hh, w.ke - key0 - 4 * w.hh);
+    }
   }
   // phase B
   if constexpr (kPV) {
@@ -580,6 +582,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   }
   const int t_begin = g_s / kBN;
   const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : t_begin;
+  // Tiles inside every row's range (they skip the mask), as scalars.  (The
+  // tile-skip test stays on vector registers: as a scalar condition it lets
+  // the compiler restructure the step so that its registers overflow.)
+  {
+    const int ms = __builtin_amdgcn_readfirstlane(w.w_max_s);
+    const int me = __builtin_amdgcn_readfirstlane(w.w_min_e);
+    w.it0 = (ms + kBN - 1) / kBN;          // first tile with key0 >= every row start
+    w.it1 = me > 0 ? me / kBN : 0;         // tiles with key0 + 64 <= every row end
+  }
 
   // ---- Q row as MFMA B operands (Q^T[d][row]); wait before any LDS load -----
   {
