@@ -59,6 +59,28 @@ int swattn_compact(const uint8_t* mask, int64_t n, int32_t* indices, int32_t* co
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Router logits -> the same two lists as swattn_compact, in one pass.
+ * No counterpart in the reference, whose router is outside its kernels
+ * (README:85, V:4-5, V:309-310): this fuses the `logits > threshold` mask
+ * a caller builds before build_switch_query_indices (V:306-322), so that
+ * neither the mask nor its extra pass over HBM exists.
+ *
+ *   logits     n values of type dtype (SWATTN_DTYPE_*), read as fp32
+ *              (bf16 and fp16 convert exactly).
+ *   threshold  position i is routed to full attention iff logits[i] >
+ *              threshold (NaN never is).  For torch parity with
+ *              `logits > t` on bf16/fp16 logits, pass t rounded to that
+ *              dtype (torch compares in the tensor's dtype).
+ *   indices, counts, workspace: as swattn_compact.
+ */
+#define SWATTN_DTYPE_F32 0
+#define SWATTN_DTYPE_BF16 1
+#define SWATTN_DTYPE_F16 2
+int swattn_compact_logits(const void* logits, int32_t dtype, int64_t n, float threshold,
+                          int32_t* indices, int32_t* counts, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
  * Index-list validation in one pass.  Replaces the device-side checks of
  * _prepare_indices (V:299-302, applied to both lists) and adds the
  * disjointness the docstring requires (V:341-342).  The count-based coverage

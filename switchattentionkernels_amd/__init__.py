@@ -9,6 +9,7 @@ Device work runs in hand-written gfx950 HIP kernels behind the C ABI of
 
 from .prefill import (  # noqa: F401
     build_switch_query_indices,
+    build_switch_query_indices_from_logits,
     switch_gqa_prefill_forward,
     switch_gqa_prefill_varlen_forward,
 )
@@ -17,6 +18,7 @@ from .flops import routed_flops  # noqa: F401
 
 __all__ = [
     "build_switch_query_indices",
+    "build_switch_query_indices_from_logits",
     "switch_gqa_prefill_forward",
     "switch_gqa_prefill_varlen_forward",
     "SwitchAttentionMetadata",

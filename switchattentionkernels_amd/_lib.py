@@ -30,6 +30,8 @@ SIGNATURES = {
     "swattn_last_error": (ctypes.c_char_p, []),
     "swattn_compact_workspace_bytes": (ctypes.c_size_t, [_i64]),
     "swattn_compact": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
+    "swattn_compact_logits": (ctypes.c_int, [_vp, _i32, _i64, ctypes.c_float, _vp, _vp, _vp,
+                                             ctypes.c_size_t, _vp]),
     "swattn_check_indices": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "swattn_build_metadata": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _i32,
                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

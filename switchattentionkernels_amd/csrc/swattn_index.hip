@@ -34,20 +34,48 @@ constexpr int kCompactThreads = kCompactWaves * 64;
 constexpr int kCompactGroups = 16;
 constexpr int kCompactChunk = kCompactThreads * kCompactGroups;  // 16384 bytes per block
 
+// What decides "full" for position i: a byte mask, or router logits above a
+// threshold (compared in fp32; bf16 and fp16 convert exactly, NaN is never
+// above the threshold).
+struct MaskSource {
+  const uint8_t* p;
+  __device__ __forceinline__ bool operator()(int64_t i) const { return p[i] != 0; }
+};
+struct F32LogitSource {
+  const float* p;
+  float thr;
+  __device__ __forceinline__ bool operator()(int64_t i) const { return p[i] > thr; }
+};
+struct BF16LogitSource {
+  const uint16_t* p;
+  float thr;
+  __device__ __forceinline__ bool operator()(int64_t i) const {
+    return __uint_as_float(static_cast<uint32_t>(p[i]) << 16) > thr;
+  }
+};
+struct F16LogitSource {
+  const _Float16* p;
+  float thr;
+  __device__ __forceinline__ bool operator()(int64_t i) const {
+    return static_cast<float>(p[i]) > thr;
+  }
+};
+
 __device__ __forceinline__ int64_t compact_elem(int wave, int e, int lane) {
   return static_cast<int64_t>(blockIdx.x) * kCompactChunk +
          static_cast<int64_t>(wave) * (64 * kCompactGroups) + 64 * e + lane;
 }
 
+template <typename Src>
 __global__ __launch_bounds__(kCompactThreads) void compact_count_kernel(
-    const uint8_t* __restrict__ mask, int64_t n, int32_t* __restrict__ block_counts) {
+    const Src src, int64_t n, int32_t* __restrict__ block_counts) {
   __shared__ int s_wave[kCompactWaves];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int cnt = 0;
 #pragma unroll
   for (int e = 0; e < kCompactGroups; ++e) {
     const int64_t i = compact_elem(wave, e, lane);
-    const bool f = i < n && mask[i] != 0;
+    const bool f = i < n && src(i);
     cnt += __builtin_popcountll(wave_ballot(f));
   }
   if (lane == 0) s_wave[wave] = cnt;
@@ -60,8 +88,9 @@ __global__ __launch_bounds__(kCompactThreads) void compact_count_kernel(
 }
 
 // block_counts == nullptr: a single block covers the whole mask.
+template <typename Src>
 __global__ __launch_bounds__(kCompactThreads) void compact_scatter_kernel(
-    const uint8_t* __restrict__ mask, int64_t n, const int32_t* __restrict__ block_counts,
+    const Src src, int64_t n, const int32_t* __restrict__ block_counts,
     int nblocks, int32_t* __restrict__ indices, int32_t* __restrict__ counts) {
   __shared__ int s_wave[kCompactWaves];
   __shared__ int s_prefix, s_total;
@@ -71,7 +100,7 @@ __global__ __launch_bounds__(kCompactThreads) void compact_scatter_kernel(
 #pragma unroll
   for (int e = 0; e < kCompactGroups; ++e) {
     const int64_t i = compact_elem(wave, e, lane);
-    const bool f = i < n && mask[i] != 0;
+    const bool f = i < n && src(i);
     bal[e] = wave_ballot(f);
     cnt += __builtin_popcountll(bal[e]);
   }
@@ -205,6 +234,10 @@ __global__ __launch_bounds__(256) void metadata_kernel(
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+template <typename Src>
+int compact_impl(const Src& src, bool src_null, int64_t n, int32_t* indices, int32_t* counts,
+                 void* workspace, size_t workspace_bytes, void* stream, const char* name);
+
 }  // namespace
 }  // namespace swattn
 
@@ -223,30 +256,30 @@ size_t swattn_compact_workspace_bytes(int64_t n) {
 
 int swattn_compact(const uint8_t* mask, int64_t n, int32_t* indices, int32_t* counts,
                    void* workspace, size_t workspace_bytes, void* stream) {
-  if (n < 0 || n > INT32_MAX) return invalid("swattn_compact: n must be in [0, 2^31)");
-  if (counts == nullptr || (n > 0 && (mask == nullptr || indices == nullptr)))
-    return invalid("swattn_compact: null pointer");
-  const hipStream_t st = as_stream(stream);
-  if (n == 0) {
-    hipLaunchKernelGGL(flags_clear_kernel, dim3(1), dim3(1), 0, st, counts);
-    hipLaunchKernelGGL(flags_clear_kernel, dim3(1), dim3(1), 0, st, counts + 1);
-    return launch_status("swattn_compact");
+  return compact_impl(MaskSource{mask}, mask == nullptr, n, indices, counts, workspace,
+                      workspace_bytes, stream, "swattn_compact");
+}
+
+int swattn_compact_logits(const void* logits, int32_t dtype, int64_t n, float threshold,
+                          int32_t* indices, int32_t* counts, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  const char* name = "swattn_compact_logits";
+  switch (dtype) {
+    case SWATTN_DTYPE_F32:
+      return compact_impl(F32LogitSource{static_cast<const float*>(logits), threshold},
+                          logits == nullptr, n, indices, counts, workspace, workspace_bytes,
+                          stream, name);
+    case SWATTN_DTYPE_BF16:
+      return compact_impl(BF16LogitSource{static_cast<const uint16_t*>(logits), threshold},
+                          logits == nullptr, n, indices, counts, workspace, workspace_bytes,
+                          stream, name);
+    case SWATTN_DTYPE_F16:
+      return compact_impl(F16LogitSource{static_cast<const _Float16*>(logits), threshold},
+                          logits == nullptr, n, indices, counts, workspace, workspace_bytes,
+                          stream, name);
+    default:
+      return invalid("swattn_compact_logits: dtype must be SWATTN_DTYPE_F32, _BF16 or _F16");
   }
-  const int64_t nb = ceil_div(n, kCompactChunk);
-  if (nb > 1) {
-    if (workspace == nullptr || workspace_bytes < swattn_compact_workspace_bytes(n)) {
-      set_error("swattn_compact: workspace too small");
-      return SWATTN_EWORKSPACE;
-    }
-    int32_t* bc = static_cast<int32_t*>(workspace);
-    hipLaunchKernelGGL(compact_count_kernel, dim3(nb), dim3(kCompactThreads), 0, st, mask, n, bc);
-    hipLaunchKernelGGL(compact_scatter_kernel, dim3(nb), dim3(kCompactThreads), 0, st, mask, n,
-                       static_cast<const int32_t*>(bc), static_cast<int>(nb), indices, counts);
-  } else {
-    hipLaunchKernelGGL(compact_scatter_kernel, dim3(1), dim3(kCompactThreads), 0, st, mask, n,
-                       static_cast<const int32_t*>(nullptr), 1, indices, counts);
-  }
-  return launch_status("swattn_compact");
 }
 
 int swattn_check_indices(const int32_t* full, int64_t n_full, const int32_t* local,
@@ -290,3 +323,39 @@ int swattn_build_metadata(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens
 }
 
 }  // extern "C"
+
+namespace swattn {
+namespace {
+
+template <typename Src>
+int compact_impl(const Src& src, bool src_null, int64_t n, int32_t* indices, int32_t* counts,
+                 void* workspace, size_t workspace_bytes, void* stream, const char* name) {
+  if (n < 0 || n > INT32_MAX) return invalid(std::string(name) + ": n must be in [0, 2^31)");
+  if (counts == nullptr || (n > 0 && (src_null || indices == nullptr)))
+    return invalid(std::string(name) + ": null pointer");
+  const hipStream_t st = as_stream(stream);
+  if (n == 0) {
+    hipLaunchKernelGGL(flags_clear_kernel, dim3(1), dim3(1), 0, st, counts);
+    hipLaunchKernelGGL(flags_clear_kernel, dim3(1), dim3(1), 0, st, counts + 1);
+    return launch_status(name);
+  }
+  const int64_t nb = ceil_div(n, kCompactChunk);
+  if (nb > 1) {
+    if (workspace == nullptr || workspace_bytes < swattn_compact_workspace_bytes(n)) {
+      set_error(std::string(name) + ": workspace too small");
+      return SWATTN_EWORKSPACE;
+    }
+    int32_t* bc = static_cast<int32_t*>(workspace);
+    hipLaunchKernelGGL(compact_count_kernel<Src>, dim3(nb), dim3(kCompactThreads), 0, st, src, n,
+                       bc);
+    hipLaunchKernelGGL(compact_scatter_kernel<Src>, dim3(nb), dim3(kCompactThreads), 0, st, src,
+                       n, static_cast<const int32_t*>(bc), static_cast<int>(nb), indices, counts);
+  } else {
+    hipLaunchKernelGGL(compact_scatter_kernel<Src>, dim3(1), dim3(kCompactThreads), 0, st, src, n,
+                       static_cast<const int32_t*>(nullptr), 1, indices, counts);
+  }
+  return launch_status(name);
+}
+
+}  // namespace
+}  // namespace swattn

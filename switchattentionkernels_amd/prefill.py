@@ -210,6 +210,51 @@ def build_switch_query_indices(full_mask: torch.Tensor) -> Tuple[torch.Tensor, t
     return full, local
 
 
+_LOGIT_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def build_switch_query_indices_from_logits(
+        router_logits: torch.Tensor, threshold: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Route and compact in one pass: full attention where ``router_logits >
+    threshold``.
+
+    Same result, bit for bit, as ``build_switch_query_indices(router_logits >
+    threshold)``, without materialising the mask.  The reference keeps its
+    router outside the kernels (README:85, V:4-5); this is the fused step in
+    front of ``build_switch_query_indices`` (V:306-322).  ``router_logits`` is
+    a device tensor of shape ``[S]``, ``[1, S]`` or ``[B, S]`` (positions then
+    flattened to ``b * S + i``) in float32, bfloat16 or float16.  As with
+    torch's ``>`` against a Python number, the threshold is first rounded to
+    the logits' dtype.
+    """
+    if router_logits.ndim == 2:
+        router_logits = router_logits.reshape(-1)
+    if (router_logits.ndim != 1 or router_logits.dtype not in _LOGIT_DTYPES
+            or not router_logits.is_cuda):
+        raise TypeError("router_logits must be a device-resident float32, bfloat16 or float16 "
+                        "tensor with shape [S], [1,S] or [B,S]")
+    n = router_logits.numel()
+    if n >= 2 ** 31:
+        raise ValueError("router_logits must hold fewer than 2^31 positions")
+    dev = router_logits.device
+    logits = router_logits.contiguous()
+    thr = float(torch.tensor(float(threshold), dtype=logits.dtype).item())
+    out = torch.empty(n, dtype=torch.int32, device=dev)
+    counts = torch.empty(2, dtype=torch.int32, device=dev)
+    L = _lib.lib()
+    ws_bytes = int(L.swattn_compact_workspace_bytes(n))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = L.swattn_compact_logits(logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], n, thr,
+                                     out.data_ptr(), counts.data_ptr(), ws.data_ptr(), ws_bytes,
+                                     _lib.stream_handle(dev))
+    _lib.check(st, "swattn_compact_logits")
+    nf = int(counts[0].item())
+    full, local = out[:nf], out[nf:]
+    _tag_compacted(full, local, n)
+    return full, local
+
+
 def switch_gqa_prefill_forward(
     q: torch.Tensor,
     k: torch.Tensor,

@@ -34,7 +34,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     funcs = _header_functions()
-    assert len(funcs) == 8, funcs
+    assert len(funcs) == 9, funcs
     lib = _lib.lib()
     for name in funcs:
         assert hasattr(lib, name), name
@@ -74,6 +74,12 @@ def test_host_side_argument_errors():
                                 1, 0, 1, 4, 4, 128, 4, ctypes.c_float(1.0), None, 0, None)
     assert st == 0
     assert lib.swattn_compact(None, -1, None, None, None, 0, None) == -1
+    dummy16 = ctypes.c_void_p(16)
+    st = lib.swattn_compact_logits(dummy16, 7, 4, ctypes.c_float(0.0), dummy16, dummy16, None, 0,
+                                   None)
+    assert st == -1 and b"dtype" in lib.swattn_last_error()
+    assert lib.swattn_compact_logits(None, 0, 4, ctypes.c_float(0.0), dummy16, dummy16, None, 0,
+                                     None) == -1
     assert lib.swattn_check_indices(None, -1, None, 0, 5, None, None) == -1
     assert lib.swattn_build_metadata(None, None, 1, 4, 4, 0, *([None] * 7), None) == -1
 
@@ -88,6 +94,8 @@ def test_api_rejects_cpu_and_dtype_errors_like_the_reference():
         sw.switch_gqa_prefill_forward(q, k, k, idx, idx[:0])
     with pytest.raises(TypeError, match="device-resident bool tensor"):
         sw.build_switch_query_indices(torch.zeros(8, dtype=torch.bool))
+    with pytest.raises(TypeError, match="float32, bfloat16 or float16"):
+        sw.build_switch_query_indices_from_logits(torch.zeros(8))
     with pytest.raises(ValueError, match="supported accelerator device"):
         sw.build_switch_attention_metadata(8, 8, device="cpu", window_size=4)
 

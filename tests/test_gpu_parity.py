@@ -22,6 +22,7 @@ from oracle import routing as R
 from switchattentionkernels_amd import (
     build_switch_attention_metadata,
     build_switch_query_indices,
+    build_switch_query_indices_from_logits,
     switch_gqa_prefill_forward,
     switch_gqa_prefill_varlen_forward,
     workloads,
@@ -124,6 +125,48 @@ def test_compact_patterns_and_2d():
     assert np.array_equal(full.cpu().numpy(), f_o) and np.array_equal(local.cpu().numpy(), l_o)
     full1, _ = build_switch_query_indices(m2[:1].to(DEV))
     assert np.array_equal(full1.cpu().numpy(), R.compact(m2[:1].numpy())[0])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 16384, 16385, 100003])
+def test_compact_logits_bit_exact(dtype, n):
+    """Fused routing equals build_switch_query_indices(logits > t) bit for bit,
+    and the numpy compaction of the same comparison."""
+    gen = torch.Generator().manual_seed(n)
+    logits = torch.randn(n, generator=gen).to(dtype)
+    if n >= 64:   # special values: NaN, +-inf, exactly the threshold
+        logits[3] = float("nan")
+        logits[5] = float("inf")
+        logits[7] = float("-inf")
+        logits[11] = 0.25
+    d = logits.to(DEV)
+    for t in (0.25, -0.7, 0.3):
+        f, l = build_switch_query_indices_from_logits(d, t)
+        fm, lm = build_switch_query_indices(d > t)
+        assert torch.equal(f, fm) and torch.equal(l, lm), (dtype, n, t)
+        ref_f, ref_l = R.compact((d > t).cpu().numpy())
+        assert np.array_equal(f.cpu().numpy(), ref_f) and np.array_equal(l.cpu().numpy(), ref_l)
+
+
+def test_compact_logits_shapes_and_rounding():
+    # [B, S] logits flatten like a [B, S] mask
+    gen = torch.Generator().manual_seed(5)
+    lg = torch.randn(3, 1000, generator=gen).to(DEV)
+    f, l = build_switch_query_indices_from_logits(lg, 0.1)
+    fm, lm = build_switch_query_indices(lg > 0.1)
+    assert torch.equal(f, fm) and torch.equal(l, lm)
+    # bf16: the threshold is rounded to bf16 first, as torch's comparison does
+    x = torch.tensor([0.3, 0.30078125, 0.2998], dtype=torch.bfloat16, device=DEV)
+    f, _ = build_switch_query_indices_from_logits(x, 0.3)
+    fm, _ = build_switch_query_indices(x > 0.3)
+    assert torch.equal(f, fm)
+    # the result feeds the forward like a compacted mask (no re-scan needed)
+    q, k, v = (t.to(DEV) for t in _qkv(5, 1, 1000, 4, 2))
+    f, l = build_switch_query_indices_from_logits(lg[0], 0.1)
+    o, lse = switch_gqa_prefill_forward(q, k, v, f, l, window_size=64)
+    fm, lm = build_switch_query_indices(lg[0] > 0.1)
+    o2, lse2 = switch_gqa_prefill_forward(q, k, v, fm, lm, window_size=64)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
 
 
 # ----------------------------------------------------------------------------
