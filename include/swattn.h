@@ -153,6 +153,39 @@ int swattn_prefill_fwd(const void* q, const void* k, const void* v,
                        int32_t heads_kv, int32_t head_dim, int32_t window, float scale_log2,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Split key ranges (context parallelism, ring passes).  No counterpart in the
+ * reference, which covers the whole key range on one device; they build on
+ * its log2 LSE export (V:15, V:236-241) and its split of query and key
+ * positions in the metadata (V:139-141, V:179-182).
+ *
+ * swattn_shard_bounds: metadata bounds for query rows at global positions
+ * q_positions[r] of one causal sequence against the key chunk
+ * [kv_start, kv_end): the legal keys [0, p] (full) or [p - window + 1, p]
+ * (local) (F:145-155), cut to the chunk and given in chunk coordinates
+ * (key g -> g - kv_start).  A row with no key in the chunk gets an empty
+ * range (start == end).  The three outputs feed swattn_prefill_fwd with K/V
+ * pointing at the chunk.
+ */
+int swattn_shard_bounds(const int32_t* q_positions, int64_t n_q, int64_t kv_start, int64_t kv_end,
+                        int32_t window, int32_t* full_starts, int32_t* local_starts,
+                        int32_t* causal_ends, void* stream);
+
+/*
+ * swattn_merge_partials: combine n_parts (1..16) partial results over
+ * disjoint key ranges into the result over their union:
+ *   M = max_i LSE_i,  w_i = 2^(LSE_i - M),  LSE = M + log2(sum w_i),
+ *   O = sum_i w_i O_i / sum_i w_i.
+ * o_parts / lse_parts are host arrays of device pointers to bf16 [rows, 128]
+ * and fp32 [rows] (rows = B*S*Hq; LSE in the log2 convention).  Parts with
+ * LSE = -inf (no legal key) carry no weight; a row empty in every part is
+ * written as O = NaN, LSE = -inf, like the attention kernel's empty rows.
+ * out / lse_out may alias neither input.
+ */
+int swattn_merge_partials(const void* const* o_parts, const float* const* lse_parts,
+                          int32_t n_parts, void* out, float* lse_out, int64_t rows,
+                          int32_t head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,6 +30,10 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``)
                            the routed result is the per-row select of the two
                            dense branches; packed == per-sequence.
 * ``routed_flops``         == a direct count of legal (query, key) pairs.
+* ``shard_bounds``         whole-sequence chunk == ``default_bounds``; the
+                           chunks of any split partition every row's range.
+* ``merge_partials``       attention over disjoint key subsets, merged, ==
+                           attention over their union (float64 brute force).
 
 Parity of the exact bf16 bits produced by the reference's TileLang kernels is
 unpinned (those kernels need TileLang + Hopper, neither exists here); the
@@ -41,6 +45,7 @@ from .routing import (  # noqa: F401
     check_indices,
     default_bounds,
     varlen_metadata,
+    shard_bounds,
     ERR_FULL_RANGE,
     ERR_FULL_ORDER,
     ERR_LOCAL_RANGE,
@@ -52,5 +57,6 @@ from .attention import (  # noqa: F401
     brute_force_attention,
     routed_flops,
     row_bounds,
+    merge_partials,
     LOG2E,
 )

@@ -167,3 +167,25 @@ def routed_flops(full_idx, local_idx, batch, seq_q, seq_kv, heads_q, head_dim,
     start, end = row_bounds(full_idx, local_idx, fs, ls, en)
     pairs = np.maximum(end - start, 0).sum()
     return int(4 * head_dim * heads_q * int(pairs))
+
+
+def merge_partials(outputs, lses):
+    """Combine attention results over disjoint key ranges (float64).
+
+    ``outputs[i]``: ``[..., D]``; ``lses[i]``: ``[...]``, log2 convention
+    (V:236-241: LSE = log2 sum_j 2^(s_j c)).  The union's LSE is
+    ``log2 sum_i 2^LSE_i`` and its output ``sum_i 2^(LSE_i - LSE) O_i``.
+    Parts with LSE = -inf (no legal key) carry no weight; a row empty in every
+    part gives NaN / -inf, as an empty row does in ``routed_attention``.
+    """
+    O = [torch.as_tensor(o, dtype=torch.float64) for o in outputs]
+    L = [torch.as_tensor(l, dtype=torch.float64) for l in lses]
+    m = torch.stack(L).amax(0)
+    live = torch.isfinite(m)
+    safe_m = torch.where(live, m, torch.zeros_like(m))
+    w = [torch.where(torch.isfinite(l), torch.exp2(l - safe_m), torch.zeros_like(l)) for l in L]
+    wsum = sum(w)
+    acc = sum(wi.unsqueeze(-1) * torch.nan_to_num(oi) for wi, oi in zip(w, O))
+    out = acc / wsum.unsqueeze(-1)
+    lse = torch.where(live, safe_m + torch.log2(wsum), torch.full_like(m, -math.inf))
+    return out, lse

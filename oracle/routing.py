@@ -142,3 +142,24 @@ def varlen_metadata(cu_seqlens_q, cu_seqlens_kv, window: int) -> dict:
         out["kv_positions"][k0:k1] = np.arange(k1 - k0)
         out["kv_segment_ids"][k0:k1] = s
     return out
+
+
+def shard_bounds(q_positions, kv_start: int, kv_end: int, window: int):
+    """Key bounds of query rows at global positions against the key chunk
+    ``[kv_start, kv_end)`` of one causal sequence, in chunk coordinates.
+
+    Global legal keys are F's rule (F:145-155): ``[0, p]`` for the full branch
+    and ``[max(p - W + 1, 0), p]`` for the local branch.  Each range is cut to
+    the chunk and shifted by ``-kv_start``; an empty cut is ``start == end``.
+    Returns (full_starts, local_starts, ends) as int64 arrays.
+    """
+    p = np.asarray(q_positions, dtype=np.int64)
+    n = kv_end - kv_start
+
+    def clip(g):
+        return np.clip(g - kv_start, 0, n)
+
+    ends = clip(p + 1)
+    full_starts = np.minimum(clip(np.zeros_like(p)), ends)
+    local_starts = np.minimum(clip(p - window + 1), ends)
+    return full_starts, local_starts, ends

@@ -15,6 +15,7 @@ from .prefill import (  # noqa: F401
 )
 from .metadata import SwitchAttentionMetadata, build_switch_attention_metadata  # noqa: F401
 from .flops import routed_flops  # noqa: F401
+from .split import merge_attention_partials, shard_attention_metadata  # noqa: F401
 
 __all__ = [
     "build_switch_query_indices",
@@ -24,4 +25,6 @@ __all__ = [
     "SwitchAttentionMetadata",
     "build_switch_attention_metadata",
     "routed_flops",
+    "shard_attention_metadata",
+    "merge_attention_partials",
 ]

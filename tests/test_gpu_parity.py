@@ -10,6 +10,7 @@ size-independent properties that must hold bit-exactly.
 """
 
 import ctypes
+import math
 import os
 import re
 
@@ -23,6 +24,8 @@ from switchattentionkernels_amd import (
     build_switch_attention_metadata,
     build_switch_query_indices,
     build_switch_query_indices_from_logits,
+    merge_attention_partials,
+    shard_attention_metadata,
     switch_gqa_prefill_forward,
     switch_gqa_prefill_varlen_forward,
     workloads,
@@ -475,3 +478,87 @@ def test_golden_fixture(name):
     assert np.array_equal(full.cpu().numpy(), z["full_idx"])
     assert np.array_equal(local.cpu().numpy(), z["local_idx"])
     _assert_close(o, lse, torch.from_numpy(z["out"]), torch.from_numpy(z["lse"]), tag=name)
+
+
+# ----------------------------------------------------------------------------
+# split key ranges (context parallelism): shard bounds, merge, end to end
+# ----------------------------------------------------------------------------
+
+def test_shard_bounds_bit_exact():
+    gen = torch.Generator().manual_seed(11)
+    s, w = 5000, 300
+    pos = torch.sort(torch.randperm(s, generator=gen)[:777]).values.to(torch.int32)
+    for c0, c1 in ((0, s), (0, 1), (100, 2000), (4999, 5000), (2500, 2500)):
+        md = shard_attention_metadata(pos.to(DEV), kv_start=c0, kv_end=c1, window_size=w)
+        fs, ls, e = R.shard_bounds(pos.numpy(), c0, c1, w)
+        assert np.array_equal(md.full_starts.cpu().numpy(), fs)
+        assert np.array_equal(md.local_starts.cpu().numpy(), ls)
+        assert np.array_equal(md.causal_ends.cpu().numpy(), e)
+
+
+def test_merge_kernel_matches_oracle():
+    gen = torch.Generator().manual_seed(12)
+    shape = (1, 300, 6)
+    outs, lses = [], []
+    for i in range(3):
+        outs.append((torch.randn(*shape, 128, generator=gen) * 2).to(torch.bfloat16))
+        l = torch.randn(*shape, generator=gen) * 20
+        l[torch.rand(*shape, generator=gen) < 0.2] = -math.inf     # parts with no key
+        lses.append(l)
+    lses[0][0, :5] = lses[1][0, :5] = lses[2][0, :5] = -math.inf   # rows empty everywhere
+    for i in range(3):   # an empty part's O is NaN, as the forward writes it
+        outs[i][torch.isneginf(lses[i])] = float("nan")
+    o, l = merge_attention_partials([x.to(DEV) for x in outs], [x.to(DEV) for x in lses])
+    o_r, l_r = oracle.merge_partials([x.float() for x in outs], lses)
+    o, l = o.float().cpu(), l.cpu()
+    assert torch.equal(torch.isnan(o), torch.isnan(o_r.float()))
+    assert torch.equal(torch.isneginf(l), torch.isneginf(l_r.float()))
+    ok = ~torch.isnan(o_r)
+    err = (o[ok].double() - o_r[ok]).abs()
+    assert (err <= 2.0 ** -8 * o_r[ok].abs() + 1e-6).all(), err.max()   # bf16 output rounding
+    fin = torch.isfinite(l_r)
+    assert ((l[fin].double() - l_r[fin]).abs() <= 1e-5 * l_r[fin].abs().clamp(min=1)).all()
+
+
+def _split_run(q, k, v, full, local, pos, chunks, w):
+    outs, lses = [], []
+    for c0, c1 in chunks:
+        md = shard_attention_metadata(pos, kv_start=c0, kv_end=c1, window_size=w)
+        o, l = switch_gqa_prefill_forward(q, k[:, c0:c1], v[:, c0:c1], full, local, metadata=md,
+                                          window_size=w)
+        outs.append(o)
+        lses.append(l)
+    return merge_attention_partials(outs, lses)
+
+
+def test_split_keys_then_merge_equals_full():
+    s, hq, hkv, w = 3000, 8, 2, 256
+    q, k, v = _qkv(13, 1, s, hq, hkv)
+    m = _mask(13, (1, s), 0.3)
+    o_full, l_full, full, local = _gpu_run(q, k, v, m, w)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    pos = torch.arange(s, dtype=torch.int32, device=DEV)
+    o_m, l_m = _split_run(qd, kd, vd, full, local, pos, ((0, 1000), (1000, 2100), (2100, s)), w)
+    o_ref, l_ref = _oracle(q, k, v, m, w)
+    _assert_close(o_m, l_m, o_ref, l_ref, tag="split-merge vs oracle")
+    _assert_close(o_m, l_m, o_full.float().cpu(), l_full.cpu(), tag="split-merge vs unsplit")
+
+
+def test_zigzag_query_shard_with_ring_merge():
+    """A zig-zag query shard (first and last 512 positions) against the full
+    keys, and against two key chunks merged, reproduces those rows."""
+    s, hq, hkv, w = 3000, 8, 2, 256
+    q, k, v = _qkv(14, 1, s, hq, hkv)
+    m = _mask(14, (1, s), 0.3)
+    o_full, l_full, _, _ = _gpu_run(q, k, v, m, w)
+    rows = torch.cat([torch.arange(512), torch.arange(s - 512, s)])
+    q_s = q[:, rows].contiguous().to(DEV)
+    f_s, l_s = build_switch_query_indices(m[:, rows].to(DEV))
+    pos = rows.to(torch.int32).to(DEV)
+    kd, vd = k.to(DEV), v.to(DEV)
+    ref_o, ref_l = o_full[:, rows.to(DEV)].float().cpu(), l_full[:, rows.to(DEV)].cpu()
+    md = shard_attention_metadata(pos, kv_start=0, kv_end=s, window_size=w)
+    o1, l1 = switch_gqa_prefill_forward(q_s, kd, vd, f_s, l_s, metadata=md, window_size=w)
+    _assert_close(o1, l1, ref_o, ref_l, tag="zig-zag shard, whole keys")
+    o2, l2 = _split_run(q_s, kd, vd, f_s, l_s, pos, ((0, 1700), (1700, s)), w)
+    _assert_close(o2, l2, ref_o, ref_l, tag="zig-zag shard, two key chunks merged")

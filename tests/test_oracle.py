@@ -339,3 +339,75 @@ def test_planted_mistakes_are_caught(monkeypatch):
     assert not _pins_pass()
     monkeypatch.setattr(A.torch, "bmm", real_bmm)
     assert _pins_pass()
+
+
+# ----------------------------------------------------------------------------
+# split key ranges: shard bounds and the log2-LSE merge
+# ----------------------------------------------------------------------------
+
+def test_shard_bounds_whole_chunk_is_the_default_rule():
+    s, w = 300, 37
+    fs, ls, e = R.shard_bounds(np.arange(s), 0, s, w)
+    dfs, dls, de = R.default_bounds(1, s, s, w)
+    assert np.array_equal(fs, dfs) and np.array_equal(ls, dls) and np.array_equal(e, de)
+
+
+def test_shard_bounds_partition_every_row():
+    s, w = 500, 64
+    gen = np.random.default_rng(0)
+    pos = np.sort(gen.choice(s, size=120, replace=False))
+    cuts = [0, 1, 63, 200, 201, 377, s]
+    gfs, gls, ge = R.shard_bounds(pos, 0, s, w)
+    for starts_g, which in ((gfs, 0), (gls, 1)):
+        covered = np.zeros(len(pos), dtype=np.int64)
+        for c0, c1 in zip(cuts[:-1], cuts[1:]):
+            b = R.shard_bounds(pos, c0, c1, w)
+            st, en = b[which], b[2]
+            assert np.all(st <= en) and np.all(en <= c1 - c0)
+            lo, hi = st + c0, en + c0
+            nonempty = hi > lo
+            assert np.all(lo[nonempty] >= np.maximum(starts_g, c0)[nonempty])
+            assert np.all(hi[nonempty] <= np.minimum(ge, c1)[nonempty])
+            covered += hi - lo
+        assert np.array_equal(covered, ge - starts_g)
+
+
+def _attend_keys(q, k, v, keys):
+    """float64 attention of each row over an explicit key list (LSE in log2)."""
+    n, d = q.shape
+    out = np.full((n, d), np.nan)
+    lse = np.full(n, -np.inf)
+    for i in range(n):
+        ks = keys[i]
+        if len(ks) == 0:
+            continue
+        sc = np.array([np.dot(q[i], k[j]) for j in ks]) / math.sqrt(d)
+        mx = sc.max()
+        wts = np.exp(sc - mx)
+        out[i] = (wts[:, None] * v[ks]).sum(0) / wts.sum()
+        lse[i] = (mx + math.log(wts.sum())) * oracle.LOG2E
+    return out, lse
+
+
+def test_merge_of_disjoint_key_sets_equals_union():
+    gen = np.random.default_rng(3)
+    n, nk, d = 30, 50, 16
+    q, k, v = gen.normal(size=(n, d)), gen.normal(size=(nk, d)), gen.normal(size=(nk, d))
+    rows = [sorted(gen.choice(nk, size=gen.integers(0, 20), replace=False)) for _ in range(n)]
+    rows[0] = []                                     # a row with no key at all
+    cuts = [0, 10, 11, 35, nk]
+    parts = []
+    for c0, c1 in zip(cuts[:-1], cuts[1:]):
+        parts.append(_attend_keys(q, k, v, [[j for j in r if c0 <= j < c1] for r in rows]))
+    o_m, l_m = oracle.merge_partials([p[0] for p in parts], [p[1] for p in parts])
+    o_u, l_u = _attend_keys(q, k, v, rows)
+    o_m, l_m = o_m.numpy(), l_m.numpy()
+    assert np.isnan(o_m[0]).all() and np.isneginf(l_m[0])
+    assert np.allclose(o_m, o_u, atol=1e-12, equal_nan=True)   # empty rows: NaN in both
+    assert np.allclose(l_m, l_u, atol=1e-12)                   # and -inf in both
+    # a natural-log merge (a plausible slip) is caught by the same check
+    lt = [torch.as_tensor(p[1]) for p in parts]
+    live = np.isfinite(l_u)
+    m = torch.stack(lt).amax(0)[live]
+    wrong = sum(torch.exp(l[live] - m) for l in lt)
+    assert not np.allclose((m + torch.log2(wrong)).numpy(), l_u[live], atol=1e-6)
