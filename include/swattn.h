@@ -186,6 +186,31 @@ int swattn_merge_partials(const void* const* o_parts, const float* const* lse_pa
                           int32_t n_parts, void* out, float* lse_out, int64_t rows,
                           int32_t head_dim, void* stream);
 
+/*
+ * Routed decode: one new query token per sequence attends its KV cache.  No
+ * counterpart in the reference, which is prefill-only; the rule is the
+ * prefill's for the last row (F:145-155): with len = cache_lens[b] (clamped
+ * to [0, cache_len]) the token sits at position len - 1 and attends keys
+ * [0, len) when full[b] != 0, else [max(len - window, 0), len).  Its own K/V
+ * must already be in the cache at position len - 1.
+ *
+ *   q        bf16 [batch, heads_q, 128]
+ *   k_cache, v_cache  bf16 [batch, cache_len, heads_kv, 128]
+ *   cache_lens int32 [batch], full uint8 [batch]        (device)
+ *   out      bf16 [batch, heads_q, 128], lse fp32 [batch, heads_q] (log2,
+ *            V:236-241); a sequence with no key gets O = NaN, LSE = -inf.
+ *   heads_q / heads_kv <= 8.  workspace >= swattn_decode_workspace_bytes(),
+ *   which depends on the current device's CU count (ask on that device).
+ * Split-K over 256-key chunks, fp32 partials merged in a second kernel.
+ */
+size_t swattn_decode_workspace_bytes(int32_t batch, int64_t cache_len, int32_t heads_q,
+                                     int32_t heads_kv);
+int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* cache_lens, const uint8_t* full, void* out, float* lse,
+                      int32_t batch, int64_t cache_len, int32_t heads_q, int32_t heads_kv,
+                      int32_t head_dim, int32_t window, float scale_log2, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

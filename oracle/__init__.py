@@ -34,6 +34,9 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``)
                            chunks of any split partition every row's range.
 * ``merge_partials``       attention over disjoint key subsets, merged, ==
                            attention over their union (float64 brute force).
+* ``decode_attention``     == the last row of ``routed_attention`` run over
+                           the cache as a sequence (full and local, W in and
+                           out of range, length 1).
 
 Parity of the exact bf16 bits produced by the reference's TileLang kernels is
 unpinned (those kernels need TileLang + Hopper, neither exists here); the
@@ -58,5 +61,6 @@ from .attention import (  # noqa: F401
     routed_flops,
     row_bounds,
     merge_partials,
+    decode_attention,
     LOG2E,
 )

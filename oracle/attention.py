@@ -189,3 +189,36 @@ def merge_partials(outputs, lses):
     out = acc / wsum.unsqueeze(-1)
     lse = torch.where(live, safe_m + torch.log2(wsum), torch.full_like(m, -math.inf))
     return out, lse
+
+
+def decode_attention(q, k_cache, v_cache, cache_lens, full_mask, *, window_size=1024,
+                     sm_scale=None):
+    """Routed decode in fp32: the prefill rule (F:145-155) for the last row.
+
+    ``q``: ``[B, Hq, D]``; caches ``[B, L, Hkv, D]``; ``cache_lens`` ``[B]``
+    (clamped to ``[0, L]``); ``full_mask`` ``[B]`` bool.  The token of sequence
+    b sits at position ``n - 1`` (``n = cache_lens[b]``) and sees keys
+    ``[0, n)`` when full, else ``[max(n - W, 0), n)``.  Returns
+    (O ``[B, Hq, D]``, LSE2 ``[B, Hq]``); a sequence with no key gives NaN /
+    -inf.
+    """
+    q = torch.as_tensor(q).float()
+    k = torch.as_tensor(k_cache).float()
+    v = torch.as_tensor(v_cache).float()
+    batch, hq, d = q.shape
+    cache_len, hkv = k.shape[1], k.shape[2]
+    g = hq // hkv
+    scale = (1.0 / d) ** 0.5 if sm_scale is None else float(sm_scale)
+    out = torch.full((batch, hq, d), math.nan)
+    lse = torch.full((batch, hq), -math.inf)
+    for b in range(batch):
+        n = max(0, min(int(cache_lens[b]), cache_len))
+        lo = 0 if bool(full_mask[b]) else max(n - window_size, 0)
+        if n <= lo:
+            continue
+        kk = k[b, lo:n].repeat_interleave(g, dim=1)   # [keys, Hq, D]
+        vv = v[b, lo:n].repeat_interleave(g, dim=1)
+        s = torch.einsum("hd,khd->hk", q[b], kk) * scale
+        lse[b] = torch.logsumexp(s, dim=1) * LOG2E
+        out[b] = torch.einsum("hk,khd->hd", torch.softmax(s, dim=1), vv)
+    return out, lse

@@ -16,6 +16,7 @@ from .prefill import (  # noqa: F401
 from .metadata import SwitchAttentionMetadata, build_switch_attention_metadata  # noqa: F401
 from .flops import routed_flops  # noqa: F401
 from .split import merge_attention_partials, shard_attention_metadata  # noqa: F401
+from .decode import switch_gqa_decode_forward  # noqa: F401
 
 __all__ = [
     "build_switch_query_indices",
@@ -27,4 +28,5 @@ __all__ = [
     "routed_flops",
     "shard_attention_metadata",
     "merge_attention_partials",
+    "switch_gqa_decode_forward",
 ]

@@ -21,7 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libswattn.so")
 ARCH = "gfx950"
 
-SOURCES = ["swattn_index.hip", "swattn_fwd.hip", "swattn_merge.hip"]
+SOURCES = ["swattn_index.hip", "swattn_fwd.hip", "swattn_merge.hip", "swattn_decode.hip"]
 
 
 def _hipcc() -> str:

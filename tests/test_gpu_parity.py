@@ -26,6 +26,7 @@ from switchattentionkernels_amd import (
     build_switch_query_indices_from_logits,
     merge_attention_partials,
     shard_attention_metadata,
+    switch_gqa_decode_forward,
     switch_gqa_prefill_forward,
     switch_gqa_prefill_varlen_forward,
     workloads,
@@ -562,3 +563,52 @@ def test_zigzag_query_shard_with_ring_merge():
     _assert_close(o1, l1, ref_o, ref_l, tag="zig-zag shard, whole keys")
     o2, l2 = _split_run(q_s, kd, vd, f_s, l_s, pos, ((0, 1700), (1700, s)), w)
     _assert_close(o2, l2, ref_o, ref_l, tag="zig-zag shard, two key chunks merged")
+
+
+# ----------------------------------------------------------------------------
+# routed decode (extension: one new token per sequence against its KV cache)
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("hq,hkv,w", [(32, 8, 1024), (40, 8, 64), (64, 8, 1), (8, 8, 300)])
+def test_decode_matches_oracle(hq, hkv, w):
+    gen = torch.Generator().manual_seed(hq + w)
+    lens = [1, 63, 64, 65, 255, 256, 257, 1000, 3000, 2048]
+    b, cache_len = len(lens), 3000
+    q = torch.randn(b, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    full = torch.rand(b, generator=gen) < 0.5
+    o, lse = switch_gqa_decode_forward(q.to(DEV), k.to(DEV), v.to(DEV),
+                                       torch.tensor(lens, dtype=torch.int32, device=DEV),
+                                       full.to(DEV), window_size=w)
+    o_r, lse_r = oracle.decode_attention(q, k, v, lens, full.tolist(), window_size=w)
+    _assert_close(o.unsqueeze(1), lse.unsqueeze(1), o_r.unsqueeze(1), lse_r.unsqueeze(1),
+                  tag=f"decode {hq}/{hkv} W{w}")
+
+
+def test_decode_clamps_lengths_and_matches_prefill_last_row():
+    gen = torch.Generator().manual_seed(31)
+    hq, hkv, cache_len, w = 16, 4, 700, 100
+    lens = [0, 5, 700, 9999, 333]
+    b = len(lens)
+    q = torch.randn(b, 1, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    full = torch.tensor([True, False, False, True, True])
+    o, lse = switch_gqa_decode_forward(q.to(DEV), k.to(DEV), v.to(DEV),
+                                       torch.tensor(lens, dtype=torch.int32, device=DEV),
+                                       full.to(DEV), window_size=w)
+    assert o.shape == (b, 1, hq, 128) and lse.shape == (b, 1, hq)
+    assert torch.isnan(o[0].float()).all() and torch.isneginf(lse[0]).all()   # no key at all
+    o_r, lse_r = oracle.decode_attention(q[:, 0], k, v, lens, full.tolist(), window_size=w)
+    _assert_close(o[1:], lse[1:], o_r[1:].unsqueeze(1), lse_r[1:].unsqueeze(1), tag="decode clamp")
+    # the same token as the last row of a prefill over its sequence (GPU prefill kernel)
+    for i in (1, 2, 4):
+        n = min(lens[i], cache_len)
+        qs = torch.randn(1, n, hq, 128, generator=gen).to(torch.bfloat16)
+        qs[0, n - 1] = q[i, 0]
+        mask = torch.zeros(1, n, dtype=torch.bool)
+        mask[0, n - 1] = bool(full[i])
+        o_p, lse_p, _, _ = _gpu_run(qs, k[i:i + 1, :n], v[i:i + 1, :n], mask, w)
+        _assert_close(o[i:i + 1], lse[i:i + 1], o_p[:, n - 1:n].float().cpu(),
+                      lse_p[:, n - 1:n].cpu(), tag=f"decode vs prefill row {i}")

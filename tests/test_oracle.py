@@ -411,3 +411,34 @@ def test_merge_of_disjoint_key_sets_equals_union():
     m = torch.stack(lt).amax(0)[live]
     wrong = sum(torch.exp(l[live] - m) for l in lt)
     assert not np.allclose((m + torch.log2(wrong)).numpy(), l_u[live], atol=1e-6)
+
+
+# ----------------------------------------------------------------------------
+# decode: the prefill rule for the last row
+# ----------------------------------------------------------------------------
+
+def test_decode_is_the_last_prefill_row():
+    gen = torch.Generator().manual_seed(21)
+    b, cache_len, hq, hkv, d = 4, 40, 4, 2, 16
+    q = torch.randn(b, hq, d, generator=gen)
+    k = torch.randn(b, cache_len, hkv, d, generator=gen)
+    v = torch.randn(b, cache_len, hkv, d, generator=gen)
+    lens = [1, 17, 40, 33]
+    for w in (1, 8, 100):
+        for full in ([True, False, True, False], [False, True, False, True]):
+            o, lse = A.decode_attention(q, k, v, lens, full, window_size=w)
+            for i, n in enumerate(lens):
+                qs = torch.randn(1, n, hq, d, generator=gen)
+                qs[0, n - 1] = q[i]
+                mask = np.zeros(n, dtype=bool)
+                mask[n - 1] = full[i]
+                f, l = R.compact(mask)
+                o_p, lse_p = A.routed_attention(qs, k[i:i + 1, :n], v[i:i + 1, :n], f, l,
+                                                window_size=w, rows=[n - 1])
+                assert torch.allclose(o[i], o_p[0, n - 1], atol=1e-5), (w, i)
+                assert torch.allclose(lse[i], lse_p[0, n - 1], atol=1e-5), (w, i)
+    # a length beyond the cache is clamped; zero keys give NaN / -inf
+    o, lse = A.decode_attention(q, k, v, [0, 99, 1, 1], [True] * 4, window_size=4)
+    assert torch.isnan(o[0]).all() and torch.isneginf(lse[0]).all()
+    o2, lse2 = A.decode_attention(q, k, v, [0, cache_len, 1, 1], [True] * 4, window_size=4)
+    assert torch.equal(o[1], o2[1]) and torch.equal(lse[1], lse2[1])
