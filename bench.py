@@ -9,9 +9,11 @@ on the CPU with a fixed seed and moved to HBM before timing.
 
 One step = one routed prefill through the public API, exactly as a caller
 runs it: build_switch_query_indices(mask) + switch_gqa_prefill_forward(...)
-(compaction, index validation with its device-to-host flag read, and the
-attention launch).  value = routed FLOPs / step time, where routed FLOPs are
-counted exactly from the mask (4*d*Hq per legal query/key pair).
+(compaction with its device-to-host count read, the checks, and the
+attention launch; lists fresh from the compaction skip the device index
+scan, which any other lists get).  value = routed FLOPs / step time, where
+routed FLOPs are counted exactly from the mask (4*d*Hq per legal query/key
+pair).
 
 The JSON line also carries:
 * roofline: the attention kernel alone, timed with HIP events on the stream it
@@ -19,8 +21,9 @@ The JSON line also carries:
 * cpu_baseline: the fp32 PyTorch oracle (a restatement of the reference's
   semantics -- the reference has no CPU path) on a bounded random row sample
   of the same workload, on this host's cores;
-* comparators: the same kernel on all-full routing (dense causal), and
-  torch SDPA causal (flash backend) on the same shape.
+* comparators: the same kernel on all-full routing (dense causal), torch
+  SDPA causal (flash backend) on the same shape, the compaction alone, and
+  the routed decode extension (64 sequences, 8192-key caches) against HBM.
 """
 
 from __future__ import annotations
@@ -182,6 +185,28 @@ def main():
         except Exception as exc:  # comparator only
             print(f"[bench] SDPA comparator unavailable: {exc}", file=sys.stderr, flush=True)
 
+    # ---- routed decode (extension): one token per sequence over its KV cache ------
+    decode = None
+    try:
+        from switchattentionkernels_amd import switch_gqa_decode_forward
+        db, dl = 64, 8192
+        gen = torch.Generator().manual_seed(args.seed)
+        dq = torch.randn(db, 1, HQ, D, generator=gen).to(torch.bfloat16).to(dev)
+        dk = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+        dv = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+        dlens = torch.full((db,), dl, dtype=torch.int32, device=dev)
+        dfull = (torch.rand(db, generator=gen) < args.p_full).to(dev)
+        dkeys = sum(dl if f else min(dl, W) for f in dfull.tolist())
+        dbytes = dkeys * HKV * D * 2 * 2 + 2 * db * HQ * D * 2
+        dec_ms = time_launches(lambda: switch_gqa_decode_forward(dq, dk, dv, dlens, dfull,
+                                                                  window_size=W), 20, warmup=5)
+        decode = {"workload": f"B{db} cache {dl} Hq{HQ}/Hkv{HKV} W{W} p_full={args.p_full}",
+                  "us": round(dec_ms * 1e3, 1), "hbm_gbs": round(dbytes / (dec_ms * 1e-3) / 1e9, 1),
+                  "hbm_frac": round(dbytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
+        del dq, dk, dv
+    except Exception as exc:  # comparator only
+        print(f"[bench] decode comparator unavailable: {exc}", file=sys.stderr, flush=True)
+
     # ---- traffic (committed rocprofv3 --pmc result, if any) ---------------------
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "fwd_s16k_p25_traffic.txt")
@@ -260,6 +285,7 @@ def main():
             "sdpa_flash_causal_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
             "compaction_us": round(compact_ms * 1e3, 2),
             "compaction_gbs": round(compact_bytes / (compact_ms * 1e-3) / 1e9, 1),
+            "decode": decode,
         },
     }
     print(json.dumps(res), flush=True)
