@@ -17,7 +17,8 @@ pair).
 
 The JSON line also carries:
 * roofline: the attention kernel alone, timed with HIP events on the stream it
-  runs on, against the 2516.6 TFLOP/s dense bf16 MFMA peak;
+  runs on, against the 2516.6 TFLOP/s dense bf16 MFMA peak, and beside it the
+  rate a register-only MFMA stream holds on this chip (swattn_mfma_peak);
 * cpu_baseline: the fp32 PyTorch oracle (a restatement of the reference's
   semantics -- the reference has no CPU path) on a bounded random row sample
   of the same workload, on this host's cores;
@@ -169,6 +170,24 @@ def main():
     print(f"[bench] attention kernel {attn_ms:.3f} ms ({attn_tflops:.1f} TFLOP/s); dense causal "
           f"{dense_ms:.3f} ms; compaction {compact_ms * 1e3:.1f} us", file=sys.stderr, flush=True)
 
+    # ---- achievable MFMA rate: register-only bf16 MFMA stream, two waves per SIMD ----
+    mfma_tflops = None
+    try:
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        blocks, iters = 2 * cus, 20000
+        probe = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+
+        def peak():
+            st = L.swattn_mfma_peak(iters, blocks, probe.data_ptr(), stream)
+            if st != 0:
+                raise RuntimeError(L.swattn_last_error().decode())
+
+        peak_ms = time_launches(peak, 5, warmup=2)
+        mfma_tflops = blocks * 4 * iters * 8 * 32768 / (peak_ms * 1e-3) / 1e12
+        print(f"[bench] MFMA-only probe {mfma_tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    except Exception as exc:  # diagnostic only
+        print(f"[bench] MFMA probe unavailable: {exc}", file=sys.stderr, flush=True)
+
     # ---- SDPA comparator (flash backend, GQA expanded) -------------------------
     sdpa_ms = None
     if not args.no_sdpa:
@@ -276,7 +295,11 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false>",
-                     "kernel_ms": round(attn_ms, 4)},
+                     "kernel_ms": round(attn_ms, 4),
+                     "achievable_mfma_tflops": None if mfma_tflops is None
+                     else round(mfma_tflops, 1),
+                     "frac_of_achievable": None if mfma_tflops is None
+                     else round(achieved / mfma_tflops, 4)},
         "cpu_baseline": cpu,
         "comparators": {
             "dense_causal_same_kernel_ms": round(dense_ms, 4),

@@ -211,6 +211,52 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
                       int32_t head_dim, int32_t window, float scale_log2, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/*
+ * Routed GQA prefill backward: dq, dk, dv of swattn_prefill_fwd's output.
+ * No counterpart in the reference, which is forward-only (V:14-15); this is
+ * the derivative of its forward (V:103-249) and consumes the log2 LSE it
+ * exports (V:236-241).  For row r (query head h, KV head h / G) and legal
+ * key j, with P = 2^(c q.k - LSE), Delta_r = dO_r . O_r and
+ * dS = P (dO_r . v_j - Delta_r):
+ *   dq_r = s sum_j dS k_j,  dk_j = s sum_r dS q_r,  dv_j = sum_r P dO_r,
+ * s = sm_scale = scale_log2 * ln 2, dk/dv summed over the group's heads.
+ *
+ *   q, k, v, full_idx/local_idx, metadata, shapes, window, scale_log2: as
+ *        passed to swattn_prefill_fwd (scale_log2 > 0).
+ *   out, lse   that call's outputs (bf16 O, fp32 log2 LSE).
+ *   dout       bf16 [batch, seq_q, heads_q, 128], the gradient of out.
+ *   dq         bf16 like q: rows listed in full_idx/local_idx are written,
+ *              others untouched; a row with no legal key gets 0.
+ *   dk, dv     bf16 like k: every key row is written (0 where no row sees it).
+ *   workspace  >= swattn_prefill_bwd_workspace_bytes(...) (depends on the
+ *              list lengths); overwritten (calls sharing it must not overlap).
+ * Each list's key bounds must be non-decreasing along the list (true for
+ * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
+ * ascending positions): the keys a row block can see are found by binary
+ * search over them.
+ */
+size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t heads_q,
+                                          int32_t heads_kv, int32_t head_dim, int64_t n_full,
+                                          int64_t n_local);
+int swattn_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
+                       const float* lse, const void* dout, const int32_t* full_idx,
+                       int64_t n_full, const int32_t* local_idx, int64_t n_local,
+                       const int32_t* full_starts, const int32_t* local_starts,
+                       const int32_t* causal_ends, void* dq, void* dk, void* dv, int32_t batch,
+                       int64_t seq_q, int64_t seq_kv, int32_t heads_q, int32_t heads_kv,
+                       int32_t head_dim, int32_t window, float scale_log2, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * Roofline diagnostic, no counterpart in the reference: `blocks` workgroups
+ * of four waves each issue iters * 8 dependent-free v_mfma_f32_32x32x16_bf16
+ * (32768 flop each) from registers, and each thread writes one float of
+ * out[blocks * 256].  Timing it gives the bf16 matrix rate the chip holds
+ * under a pure MFMA load (the clock drops below the one the published peak
+ * assumes), against which the attention kernel's rate can be read.
+ */
+int swattn_mfma_peak(int64_t iters, int32_t blocks, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,8 +13,9 @@ Modules
               (V:271-304, V:390-393), position metadata (V:27, V:353-383,
               F:145-155).  numpy, bit-exact.
 ``attention`` floating-point work: dense masked attention in fp32 torch
-              (V:103-249), plus a float64 pure-Python brute force for tiny
-              inputs used to pin the fp32 restatement.
+              (V:103-249) and its backward (the derivative of that
+              forward; the reference has none, V:14-15), plus a float64
+              pure-Python brute force for tiny inputs used to pin both.
 
 Pinning (how each function is checked, see ``tests/test_oracle.py``)
 --------------------------------------------------------------------
@@ -37,6 +38,13 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``)
 * ``decode_attention``     == the last row of ``routed_attention`` run over
                            the cache as a sequence (full and local, W in and
                            out of range, length 1).
+* ``routed_attention_backward``
+                           == torch autograd through ``routed_attention``;
+                           == central finite differences (float64) of the
+                           pure-Python brute force, which shares no code with
+                           it; sum_j dk_j = 0 and sum_j dv_j = sum_i dO_i per
+                           KV head (softmax shift invariance, rows of P sum
+                           to one).
 
 Parity of the exact bf16 bits produced by the reference's TileLang kernels is
 unpinned (those kernels need TileLang + Hopper, neither exists here); the
@@ -62,5 +70,6 @@ from .attention import (  # noqa: F401
     row_bounds,
     merge_partials,
     decode_attention,
+    routed_attention_backward,
     LOG2E,
 )

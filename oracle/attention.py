@@ -12,6 +12,9 @@ Semantics restated (V:103-249):
   (log2 convention, V:236-241);
 * rows are written back to their own positions (V:243-249).
 
+``routed_attention_backward`` is the derivative of that forward (the reference
+itself is forward-only, V:14-15).
+
 The restatement is a dense masked computation in fp32 on the CPU -- no online
 softmax, no bf16 rounding of P -- so it is the exact-arithmetic target that
 the kernels are compared against within a tolerance.
@@ -222,3 +225,75 @@ def decode_attention(q, k_cache, v_cache, cache_lens, full_mask, *, window_size=
         lse[b] = torch.logsumexp(s, dim=1) * LOG2E
         out[b] = torch.einsum("hk,khd->hd", torch.softmax(s, dim=1), vv)
     return out, lse
+
+
+def _score_grad(p, dp):
+    """dS = P * (dP - rowsum(P * dP)): the softmax Jacobian applied to dP."""
+    return p * (dp - (p * dp).sum(-1, keepdim=True))
+
+
+def routed_attention_backward(q, k, v, grad_out, full_idx, local_idx, *, window_size=1024,
+                              metadata=None, sm_scale=None, chunk=256, dtype=torch.float32,
+                              rows=None):
+    """Gradients of the routed attention output, dense and masked, in ``dtype``.
+
+    The reference is forward-only (V:14-15); this is the derivative of the
+    forward restated in ``routed_attention`` (V:103-249) with respect to q, k
+    and v, for a loss whose gradient with respect to O is ``grad_out``:
+
+    * ``P = softmax(scale * q.k)`` over each row's legal keys (0 elsewhere),
+      ``dP = dO . v``, ``Delta = rowsum(P * dP)``, ``dS = P * (dP - Delta)``;
+    * ``dq = scale * dS k``, ``dk = scale * dS^T q``, ``dv = P^T dO``, the last
+      two summed over the query heads that share a KV head (V:124).
+
+    A row with no legal key has P = 0 and contributes nothing.  Inputs are CPU
+    tensors of the forward's shapes; returns ``(dq, dk, dv)`` in ``dtype``.
+    ``rows`` (optional) restricts the work to those flattened query rows: dq
+    is then exact on them (0 elsewhere) and dk / dv hold only their share.
+    """
+    batch, seq_q, hq, d = (int(x) for x in q.shape)
+    hkv = int(k.shape[2])
+    g = hq // hkv
+    scale = (1.0 / d) ** 0.5 if sm_scale is None else float(sm_scale)
+    start, end = _bounds_for(q, k, full_idx, local_idx, window_size, metadata)
+    qf = q.reshape(batch * seq_q, hq, d).to(dtype)
+    kf = k.reshape(-1, hkv, d).to(dtype)
+    vf = v.reshape(-1, hkv, d).to(dtype)
+    dof = grad_out.reshape(batch * seq_q, hq, d).to(dtype)
+    dq = torch.zeros_like(qf)
+    dk = torch.zeros_like(kf)
+    dv = torch.zeros_like(vf)
+    if rows is None:
+        rows = np.concatenate([np.asarray(full_idx, dtype=np.int64).reshape(-1),
+                               np.asarray(local_idx, dtype=np.int64).reshape(-1)])
+    rows = np.sort(np.asarray(rows, dtype=np.int64))
+    for c0 in range(0, rows.size, chunk):
+        r = rows[c0:c0 + chunk]
+        ks, ke = int(start[r].min()), int(end[r].max())
+        if ke <= ks:
+            continue
+        n = len(r)
+        rt = torch.from_numpy(r)
+        span = torch.arange(ks, ke)
+        legal = (span[None, :] >= torch.from_numpy(start[r])[:, None]) & \
+                (span[None, :] < torch.from_numpy(end[r])[:, None])          # [R, L]
+        qr = qf[rt].reshape(n, hkv, g, d).permute(1, 0, 2, 3).reshape(hkv, n * g, d)
+        dor = dof[rt].reshape(n, hkv, g, d).permute(1, 0, 2, 3).reshape(hkv, n * g, d)
+        kc = kf[ks:ke].permute(1, 0, 2).contiguous()                        # [Hkv, L, D]
+        vc = vf[ks:ke].permute(1, 0, 2).contiguous()
+        s = torch.bmm(qr, kc.transpose(1, 2).contiguous()) * scale          # [Hkv, R*G, L]
+        s = s.reshape(hkv, n, g, -1).masked_fill(~legal[None, :, None, :], float("-inf"))
+        mx = s.amax(-1, keepdim=True)
+        mx = torch.where(torch.isfinite(mx), mx, torch.zeros_like(mx))
+        e = torch.exp(s - mx)
+        tot = e.sum(-1, keepdim=True)
+        p = torch.where(tot > 0, e / torch.where(tot > 0, tot, torch.ones_like(tot)),
+                        torch.zeros_like(e)).reshape(hkv, n * g, -1)       # [Hkv, R*G, L]
+        dp = torch.bmm(dor, vc.transpose(1, 2).contiguous())                # [Hkv, R*G, L]
+        ds = _score_grad(p, dp)
+        dq_r = torch.bmm(ds, kc) * scale                                    # [Hkv, R*G, D]
+        dq[rt] = dq_r.reshape(hkv, n, g, d).permute(1, 0, 2, 3).reshape(n, hq, d)
+        dk[ks:ke] += (torch.bmm(ds.transpose(1, 2).contiguous(), qr) * scale).permute(1, 0, 2)
+        dv[ks:ke] += torch.bmm(p.transpose(1, 2).contiguous(), dor).permute(1, 0, 2)
+    return (dq.reshape(batch, seq_q, hq, d), dk.reshape(k.shape[0], -1, hkv, d),
+            dv.reshape(v.shape[0], -1, hkv, d))

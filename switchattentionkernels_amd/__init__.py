@@ -17,6 +17,11 @@ from .metadata import SwitchAttentionMetadata, build_switch_attention_metadata  
 from .flops import routed_flops  # noqa: F401
 from .split import merge_attention_partials, shard_attention_metadata  # noqa: F401
 from .decode import switch_gqa_decode_forward  # noqa: F401
+from .backward import (  # noqa: F401
+    SwitchGQAPrefillFunction,
+    switch_gqa_prefill,
+    switch_gqa_prefill_backward,
+)
 
 __all__ = [
     "build_switch_query_indices",
@@ -29,4 +34,7 @@ __all__ = [
     "shard_attention_metadata",
     "merge_attention_partials",
     "switch_gqa_decode_forward",
+    "switch_gqa_prefill_backward",
+    "switch_gqa_prefill",
+    "SwitchGQAPrefillFunction",
 ]

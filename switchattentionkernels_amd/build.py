@@ -21,7 +21,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libswattn.so")
 ARCH = "gfx950"
 
-SOURCES = ["swattn_index.hip", "swattn_fwd.hip", "swattn_merge.hip", "swattn_decode.hip"]
+SOURCES = ["swattn_index.hip", "swattn_fwd.hip", "swattn_merge.hip", "swattn_decode.hip",
+           "swattn_bwd.hip", "swattn_diag.hip"]
 
 
 def _hipcc() -> str:

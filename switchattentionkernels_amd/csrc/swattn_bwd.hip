@@ -1,0 +1,797 @@
+// Routed GQA prefill backward for gfx950 (MI355X): dQ, dK, dV of both Switch
+// Attention branches from the forward's output and log2 LSE.
+//
+// Reference tags: V = swiattn_gqa_prefill_varlen.py, F = swiattn_gqa_prefill.py.
+// The reference is forward-only (V:14-15); this is the derivative of its
+// forward (V:103-249): per query row r (query head h of KV head h / G) and
+// legal key j (V:134-137, V:186-196; F:145-155 without metadata),
+//   P[r,j] = 2^(c * q_r.k_j - LSE_r)         (log2 LSE exported at V:236-241)
+//   Delta_r = dO_r . O_r,   dS[r,j] = P[r,j] * (dO_r . v_j - Delta_r)
+//   dq_r = s * sum_j dS[r,j] k_j,  dk_j = s * sum_r dS[r,j] q_r,
+//   dv_j = sum_r P[r,j] dO_r        (s = sm_scale = c * ln 2)
+// with dk_j / dv_j summed over the G query heads of the KV head.
+//
+// Design (MI355X-first):
+// * Rows are packed as in the forward (compacted query slot, head of the
+//   group; head fastest), in blocks of 32.  bwd_prep_kernel computes Delta
+//   once per row and writes, per (branch, KV head, block), Q and dO as
+//   row-major 8 KiB blocks (A operands of S = Q K^T and dP = dO V^T) and as
+//   transposed 8 KiB blocks with the rows of each 16-row group in perm16
+//   order (A operands of dK^T = Q^T dS and dV^T = dO^T P, whose B operands
+//   are then the S / dP accumulators themselves), plus a 1 KiB block of row
+//   info (LSE, Delta, key bounds, and the block's bounds summary).
+// * bwd_dkdv_kernel: one workgroup per (128-key tile, KV head); each wave
+//   keeps its 32 keys' K and V as MFMA B operands in registers and dK^T,
+//   dV^T (128 d x 32 keys each) in accumulators, and streams the row blocks
+//   that can see the tile (a contiguous block range per branch, found by
+//   bwd_ranges_kernel with a binary search over the monotone row bounds)
+//   through a two-slot LDS ring filled by buffer_load ... lds.  Four MFMA
+//   products per block: S, dP, dV^T += dO^T P, dK^T += Q^T dS.
+// * bwd_dq_kernel: one workgroup per (128-row tile, KV head), the forward's
+//   shape: each wave owns 32 rows, keeps Q^T and dO^T as B operands, and
+//   streams K, V and K^T tiles (K^T packed like the forward's V^T) through a
+//   two-slot LDS ring.  Three products per 64-key tile: S^T = K Q^T,
+//   dP^T = V dO^T, dQ^T += K^T dS^T (dS^T as B operand straight from the
+//   accumulator, keys permuted within 16-key groups on both sides).
+// * Keys outside a row's range get S = -inf, so P = 0 exactly; a row with no
+//   legal key (or a padding row) carries LSE = Delta = 0 and bounds [0, 0),
+//   is masked everywhere and contributes nothing.
+// * dQ is a separate pass (S and dP recomputed) rather than atomics from the
+//   key-stationary pass, so every output is written once, deterministically.
+
+#include <limits.h>
+#include <math.h>
+
+#include "tiles.h"
+
+namespace swattn {
+namespace {
+
+using namespace tiles;
+
+constexpr int kThreads = 256;                          // four waves
+constexpr int kBRows = 32;                             // rows per packed block
+constexpr int kBlockBytes = kBRows * kRowBytes;        // 8 KiB row-major or transposed block
+constexpr int kTRowBytes = kBRows * 2;                 // 64-byte transposed rows (one d, 32 rows)
+constexpr int kInfoBytes = 1024;                       // row info block
+constexpr int kInfoLse = 0, kInfoDelta = 32, kInfoStart = 64, kInfoEnd = 96;   // word offsets
+constexpr int kInfoMaxStart = 128, kInfoMinEnd = 129;
+constexpr int kKeysDkv = 128;                          // keys per dK/dV workgroup (32 per wave)
+constexpr int kRowsPerItem = 128;                      // rows per dQ workgroup (32 per wave)
+// dK/dV LDS stage: Q block, dO block, Q^T block, dO^T block, info.
+constexpr int kStageBytes = 4 * kBlockBytes + kInfoBytes;
+constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffQT = 2 * kBlockBytes, kOffDOT = 3 * kBlockBytes;
+constexpr int kOffInfo = 4 * kBlockBytes;
+// dQ LDS stage: K tile, V tile, K^T tile (16 KiB each).
+constexpr int kQStageBytes = 3 * kTileBytes;
+
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  const float* lse;
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  const int32_t* idx[2];     // [0] full list, [1] local list
+  const int32_t* starts[2];  // metadata starts per branch (kMeta only)
+  const int32_t* ends;       // metadata causal ends (kMeta only)
+  int32_t count[2];          // slots per branch
+  int32_t nrows[2];          // count * G
+  int32_t blocks[2];         // ceil(nrows / 32)
+  int32_t items[2];          // ceil(nrows / 128)
+  int64_t blk_base[2];       // packed block of (branch b, head h, block i): blk_base[b] + h * blocks[b] + i
+  char* info;                // [blocks][1 KiB]
+  uint16_t* qp;              // [blocks][32 rows][128]
+  uint16_t* dop;
+  uint16_t* qt;              // [blocks][128 d][32 rows, perm16 in each 16-row group]
+  uint16_t* dot;
+  uint16_t* kt;              // K^T tiles [Hkv][kv_tiles][128][64]
+  int32_t* ranges;           // [2][kv_tiles128][2] block ranges
+  int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles128;
+  int32_t hq, hkv, group, window;
+  float c;                   // sm_scale * log2(e)
+  float scale;               // sm_scale
+};
+
+// Transposed-block chunk swizzle: four 64-byte rows share a 256-byte bank
+// line, and (d >> 2) & 3 gives the four rows of each line position four
+// distinct chunks, so 16 lanes reading one chunk of 16 consecutive d rows
+// are conflict-free.
+__device__ __forceinline__ int tswz(int d) { return (d >> 2) & 3; }
+
+template <bool kMeta>
+__device__ __forceinline__ void row_bounds(const BwdParams& p, int branch, int pos, int& ks,
+                                           int& ke) {
+  if constexpr (kMeta) {
+    ks = p.starts[branch][pos];
+    ke = p.ends[pos];
+  } else {
+    const int b = pos / p.seq_q;
+    const int i = pos - b * p.seq_q;
+    const int base = b * p.seq_kv;
+    ke = base + min(i + 1, p.seq_kv);
+    ks = branch == 0 ? base : base + max(i - p.window + 1, 0);
+  }
+  ks = max(ks, 0);
+  ke = min(ke, p.total_kv);
+}
+
+__device__ __forceinline__ int64_t packed_block(const BwdParams& p, int b, int kvh, int blk) {
+  return p.blk_base[b] + static_cast<int64_t>(kvh) * p.blocks[b] + blk;
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// ---------------------------------------------------------------------------
+// Preparation: one workgroup per (branch, block of 32 rows, KV head).
+// ---------------------------------------------------------------------------
+template <bool kMeta>
+__global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
+  __shared__ uint16_t sq[kBRows][kD + 8];   // 272-byte rows
+  __shared__ uint16_t sdo[kBRows][kD + 8];
+  __shared__ int s_ks[kBRows], s_ke[kBRows];
+  const int x = blockIdx.x, kvh = blockIdx.y;
+  const int b = x < p.blocks[0] ? 0 : 1;
+  const int blk = x - (b ? p.blocks[0] : 0);
+  const int64_t pb = packed_block(p, b, kvh, blk);
+  const int tid = threadIdx.x;
+  const int rr = tid >> 3, part = tid & 7;   // row in block, 16 d values per thread
+  const int r = blk * kBRows + rr;
+  const int G = p.group;
+  const bool valid = r < p.nrows[b];
+  int pos = 0, qh = 0, ks = 0, ke = 0;
+  if (valid) {
+    const int slot = r / G;
+    qh = kvh * G + (r - slot * G);
+    pos = p.idx[b][slot];
+    row_bounds<kMeta>(p, b, pos, ks, ke);
+  }
+  const bool live = valid && ks < ke;
+  uint4 qv[2], dv[2], ov[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) qv[i] = dv[i] = ov[i] = make_uint4(0, 0, 0, 0);
+  if (valid) {
+    const int64_t off = (static_cast<int64_t>(pos) * p.hq + qh) * kD + 16 * part;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      qv[i] = *reinterpret_cast<const uint4*>(p.q + off + 8 * i);
+      dv[i] = *reinterpret_cast<const uint4*>(p.dout + off + 8 * i);
+      ov[i] = *reinterpret_cast<const uint4*>(p.o + off + 8 * i);
+    }
+  }
+  float delta = 0.f;
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t dw[4] = {dv[i].x, dv[i].y, dv[i].z, dv[i].w};
+      const uint32_t ow[4] = {ov[i].x, ov[i].y, ov[i].z, ov[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        delta += bf16_lo(dw[e]) * bf16_lo(ow[e]) + bf16_hi(dw[e]) * bf16_hi(ow[e]);
+    }
+  }
+  delta += __shfl_xor(delta, 1);
+  delta += __shfl_xor(delta, 2);
+  delta += __shfl_xor(delta, 4);
+
+  uint16_t* qp = p.qp + pb * (kBlockBytes / 2) + rr * kD + 16 * part;
+  uint16_t* dop = p.dop + pb * (kBlockBytes / 2) + rr * kD + 16 * part;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    *reinterpret_cast<uint4*>(qp + 8 * i) = qv[i];
+    *reinterpret_cast<uint4*>(dop + 8 * i) = dv[i];
+    *reinterpret_cast<uint4*>(&sq[rr][16 * part + 8 * i]) = qv[i];
+    *reinterpret_cast<uint4*>(&sdo[rr][16 * part + 8 * i]) = dv[i];
+  }
+  if (part == 0) {
+    float* inf = reinterpret_cast<float*>(p.info + pb * kInfoBytes);
+    int* infi = reinterpret_cast<int*>(inf);
+    inf[kInfoLse + rr] = live ? p.lse[static_cast<int64_t>(pos) * p.hq + qh] : 0.f;
+    inf[kInfoDelta + rr] = live ? delta : 0.f;
+    infi[kInfoStart + rr] = live ? ks : 0;
+    infi[kInfoEnd + rr] = live ? ke : 0;
+    s_ks[rr] = live ? ks : INT_MAX;   // a dead row forces the mask on its block
+    s_ke[rr] = live ? ke : INT_MIN;
+  }
+  __syncthreads();
+  // Transposed blocks: row d holds the 32 rows' values of d; position t of
+  // each 16-row group holds row perm16(t) of the group.
+  uint16_t* qt = p.qt + pb * (kBlockBytes / 2);
+  uint16_t* dot = p.dot + pb * (kBlockBytes / 2);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int chunk = tid + kThreads * i;   // 128 d rows x 4 chunks of 8 positions
+    const int d = chunk >> 2, c = chunk & 3;
+    uint32_t wq[4], wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int p0 = 8 * c + 2 * e;
+      const int r0 = (p0 & ~15) + perm16(p0 & 15), r1 = (p0 & ~15) + perm16((p0 + 1) & 15);
+      wq[e] = static_cast<uint32_t>(sq[r0][d]) | (static_cast<uint32_t>(sq[r1][d]) << 16);
+      wd[e] = static_cast<uint32_t>(sdo[r0][d]) | (static_cast<uint32_t>(sdo[r1][d]) << 16);
+    }
+    *reinterpret_cast<uint4*>(qt + d * kBRows + 8 * c) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+    *reinterpret_cast<uint4*>(dot + d * kBRows + 8 * c) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+  if (tid == 0) {
+    int ms = INT_MIN, me = INT_MAX;
+    for (int i = 0; i < kBRows; ++i) {
+      ms = max(ms, s_ks[i]);
+      me = min(me, s_ke[i]);
+    }
+    int* infi = reinterpret_cast<int*>(p.info + pb * kInfoBytes);
+    infi[kInfoMaxStart] = ms;
+    infi[kInfoMinEnd] = me;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block ranges: for each branch and 128-key tile, the packed blocks whose
+// rows can see a key of the tile.  Row bounds are non-decreasing along each
+// list, so the slots that overlap [k0, k1) are [first with end > k0, first
+// with start >= k1).
+// ---------------------------------------------------------------------------
+template <bool kMeta>
+__global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * p.kv_tiles128) return;
+  const int b = i / p.kv_tiles128, t = i - b * p.kv_tiles128;
+  const int k0 = t * kKeysDkv, k1 = min(k0 + kKeysDkv, p.total_kv);
+  const int n = p.count[b];
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    int ks, ke;
+    row_bounds<kMeta>(p, b, p.idx[b][mid], ks, ke);
+    if (ke > k0) hi = mid; else lo = mid + 1;
+  }
+  const int s_lo = lo;
+  hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    int ks, ke;
+    row_bounds<kMeta>(p, b, p.idx[b][mid], ks, ke);
+    if (ks >= k1) hi = mid; else lo = mid + 1;
+  }
+  const int s_hi = lo;
+  int blo = 0, bhi = 0;
+  if (s_lo < s_hi) {
+    const int64_t G = p.group;
+    blo = static_cast<int>((s_lo * G) / kBRows);
+    bhi = static_cast<int>((s_hi * G + kBRows - 1) / kBRows);
+  }
+  p.ranges[2 * i] = blo;
+  p.ranges[2 * i + 1] = bhi;
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: one workgroup per (128-key tile, KV head).
+// ---------------------------------------------------------------------------
+struct DkvPlan {
+  uint32_t off[8];   // this lane's source offset inside its wave's 8 KiB block, per 1 KiB load
+};
+
+// Wave w stages block part w: 0 = Q, 1 = dO (row-major, 256-byte rows,
+// chunk swizzle swz), 2 = Q^T, 3 = dO^T (64-byte rows, swizzle tswz).  Lane l
+// of load i lands on byte 16 * (64 i + l) of the part and fetches the
+// logical chunk that belongs there.
+__device__ __forceinline__ DkvPlan make_dkv_plan(int wave, int lane) {
+  DkvPlan pl;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = 64 * i + lane;
+    if (wave < 2) {
+      const int row = c >> 4;
+      pl.off[i] = static_cast<uint32_t>(row * kRowBytes + (((c & 15) ^ swz(row)) << 4));
+    } else {
+      const int d = c >> 2;
+      pl.off[i] = static_cast<uint32_t>(d * kTRowBytes + (((c & 3) ^ tswz(d)) << 4));
+    }
+  }
+  return pl;
+}
+
+__device__ __forceinline__ void stage_dkv(const BwdParams& p, const DkvPlan& pl, int wave,
+                                          int lane, int64_t pb, uint32_t slot) {
+  const uint16_t* src = wave == 0 ? p.qp : wave == 1 ? p.dop : wave == 2 ? p.qt : p.dot;
+  const i32x4 rs = make_rsrc(src + pb * (kBlockBytes / 2), kBlockBytes);
+  const uint32_t dst = slot + wave * kBlockBytes;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
+  if (wave == 0) {
+    const i32x4 ri = make_rsrc(p.info + pb * kInfoBytes, kInfoBytes);
+    dma16(ri, static_cast<uint32_t>(16 * lane), __builtin_amdgcn_readfirstlane(slot + kOffInfo));
+  }
+}
+
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(1, 1))) void bwd_dkdv_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int t = blockIdx.x / p.hkv, kvh = blockIdx.x - (blockIdx.x / p.hkv) * p.hkv;
+  const int kw0 = t * kKeysDkv + 32 * wave;   // this wave's first key
+  const int key = kw0 + n;                    // this lane's key (B column)
+
+  // K and V of this lane's key as B operands: k-step kk holds d 16kk+8h .. +7.
+  bf16x8 kf[8], vf[8];
+  if (key < p.total_kv) {
+    const int64_t base = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      kf[kk] = *reinterpret_cast<const bf16x8*>(p.k + base + 16 * kk);
+      vf[kk] = *reinterpret_cast<const bf16x8*>(p.v + base + 16 * kk);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) kf[kk] = vf[kk] = bf16x8{};
+  }
+  f32x16 dkt[4], dvt[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) dkt[d] = dvt[d] = f32x16{};
+
+  const int b0lo = p.ranges[2 * t], b0hi = p.ranges[2 * t + 1];
+  const int b1lo = p.ranges[2 * (p.kv_tiles128 + t)], b1hi = p.ranges[2 * (p.kv_tiles128 + t) + 1];
+  const int n0 = max(b0hi - b0lo, 0), n1 = max(b1hi - b1lo, 0);
+  const int nb = n0 + n1;
+  auto block_of = [&](int i) -> int64_t {
+    return i < n0 ? packed_block(p, 0, kvh, b0lo + i) : packed_block(p, 1, kvh, b1lo + i - n0);
+  };
+
+  const DkvPlan pl = make_dkv_plan(wave, lane);
+  const uint32_t lds0 = lds_addr(smem);
+  // Operand offsets: Q / dO rows (A of S, dP): row n, chunk 2kk + h;
+  // Q^T / dO^T rows (A of dK^T, dV^T): d row 32 dblk + n, chunk 2 s2 + h.
+  int aoff[8], toff[2];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) aoff[kk] = n * kRowBytes + (((2 * kk + h) ^ swz(n)) << 4);
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) toff[s2] = n * kTRowBytes + (((2 * s2 + h) ^ tswz(n)) << 4);
+
+  if (nb > 0) stage_dkv(p, pl, wave, lane, block_of(0), lds0);
+  for (int i = 0; i < nb; ++i) {
+    // Block i is in LDS once every wave's loads are complete; every wave has
+    // finished block i-1, whose slot the next loads overwrite.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (i + 1 < nb) stage_dkv(p, pl, wave, lane, block_of(i + 1), lds0 + ((i + 1) & 1) * kStageBytes);
+    const char* sb = smem + (i & 1) * kStageBytes;
+    const float* inf = reinterpret_cast<const float*>(sb + kOffInfo);
+    const int* infi = reinterpret_cast<const int*>(inf);
+
+    f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8 aq = *reinterpret_cast<const bf16x8*>(sb + kOffQ + aoff[kk]);
+      const bf16x8 ad = *reinterpret_cast<const bf16x8*>(sb + kOffDO + aoff[kk]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[kk], s, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[kk], dp, 0, 0, 0);
+    }
+    // Element e of the accumulators is row 8(e/4) + 4h + e%4 of the block.
+    const bool interior = infi[kInfoMaxStart] <= kw0 && infi[kInfoMinEnd] >= kw0 + 32;
+    if (!interior) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int4 st = *reinterpret_cast<const int4*>(infi + kInfoStart + 8 * j + 4 * h);
+        const int4 en = *reinterpret_cast<const int4*>(infi + kInfoEnd + 8 * j + 4 * h);
+        if (key < st.x || key >= en.x) s[4 * j + 0] = -INFINITY;
+        if (key < st.y || key >= en.y) s[4 * j + 1] = -INFINITY;
+        if (key < st.z || key >= en.z) s[4 * j + 2] = -INFINITY;
+        if (key < st.w || key >= en.w) s[4 * j + 3] = -INFINITY;
+      }
+    }
+    bf16x8 pk[2], dsk[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float4 l4 = *reinterpret_cast<const float4*>(inf + kInfoLse + 8 * j + 4 * h);
+      const float4 d4 = *reinterpret_cast<const float4*>(inf + kInfoDelta + 8 * j + 4 * h);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(s[4 * j + e], p.c, -lv[e]));
+        const float ds = pe * (dp[4 * j + e] - dv[e]);
+        pk[j >> 1][4 * (j & 1) + e] = static_cast<__bf16>(pe);
+        dsk[j >> 1][4 * (j & 1) + e] = static_cast<__bf16>(ds);
+      }
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int o = toff[s2] + 32 * d * kTRowBytes;
+        const bf16x8 ado = *reinterpret_cast<const bf16x8*>(sb + kOffDOT + o);
+        const bf16x8 aqt = *reinterpret_cast<const bf16x8*>(sb + kOffQT + o);
+        dvt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ado, pk[s2], dvt[d], 0, 0, 0);
+        dkt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aqt, dsk[s2], dkt[d], 0, 0, 0);
+      }
+    }
+  }
+
+  // dK^T / dV^T element e of block d is d-row 32d + 8(e/4) + 4h + e%4 of key.
+  if (key < p.total_kv) {
+    const int64_t base = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 4 * h;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint2 uk, uv;
+        uk.x = pack_bf16x2(dkt[d][4 * j + 0] * p.scale, dkt[d][4 * j + 1] * p.scale);
+        uk.y = pack_bf16x2(dkt[d][4 * j + 2] * p.scale, dkt[d][4 * j + 3] * p.scale);
+        uv.x = pack_bf16x2(dvt[d][4 * j + 0], dvt[d][4 * j + 1]);
+        uv.y = pack_bf16x2(dvt[d][4 * j + 2], dvt[d][4 * j + 3]);
+        *reinterpret_cast<uint2*>(p.dk + base + 32 * d + 8 * j) = uk;
+        *reinterpret_cast<uint2*>(p.dv + base + 32 * d + 8 * j) = uv;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: one workgroup per (branch, 128-row tile, KV head).
+// ---------------------------------------------------------------------------
+struct DqPlan {
+  uint32_t koff[4];   // K / V row chunk offsets from the tile's first key row
+  uint32_t toff[4];   // K^T chunk offsets inside the K^T tile
+  uint32_t lds_w;     // this wave's byte offset inside a 16 KiB tile
+};
+
+// Wave w stages key rows 16w .. 16w+15 of K and V and d rows 32w .. 32w+31
+// of K^T, 1 KiB (4 key rows / 8 d rows) per load; lane l lands on 16-byte
+// position l of the load and fetches the logical chunk that belongs there.
+__device__ __forceinline__ DqPlan make_dq_plan(const BwdParams& p, int kvh, int wave, int lane) {
+  DqPlan pl;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int j = (lane & 15) ^ swz(row);
+    pl.koff[i] = static_cast<uint32_t>(((row * p.hkv + kvh) * kD + 8 * j) * 2);
+    const int d = 32 * wave + 8 * i + (lane >> 3);
+    const int jv = (lane & 7) ^ vswz(d);
+    pl.toff[i] = static_cast<uint32_t>((d * kBN + 8 * jv) * 2);
+  }
+  pl.lds_w = 16 * wave * kRowBytes;
+  return pl;
+}
+
+__device__ __forceinline__ void stage_dq(const BwdParams& p, const DqPlan& pl, int kvh, int tk,
+                                         uint32_t slot) {
+  const int64_t row_bytes = static_cast<int64_t>(p.hkv) * kD * 2;
+  const int64_t rest = (static_cast<int64_t>(p.total_kv) - static_cast<int64_t>(tk) * kBN) * row_bytes;
+  const uint32_t nrec = static_cast<uint32_t>(rest < 0xffffffffLL ? rest : 0xffffffffLL);
+  const int64_t kv_off = static_cast<int64_t>(tk) * kBN * row_bytes;
+  const i32x4 rk = make_rsrc(reinterpret_cast<const char*>(p.k) + kv_off, nrec);
+  const i32x4 rv = make_rsrc(reinterpret_cast<const char*>(p.v) + kv_off, nrec);
+  const i32x4 rt = make_rsrc(reinterpret_cast<const char*>(p.kt) +
+                                 (static_cast<int64_t>(kvh) * p.kv_tiles + tk) * kTileBytes,
+                             kTileBytes);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t o = slot + pl.lds_w + 4 * i * kRowBytes;
+    dma16(rk, pl.koff[i], __builtin_amdgcn_readfirstlane(o));
+    dma16(rv, pl.koff[i], __builtin_amdgcn_readfirstlane(o + kTileBytes));
+    dma16(rt, pl.toff[i], __builtin_amdgcn_readfirstlane(o + 2 * kTileBytes));
+  }
+}
+
+__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
+                          amdgpu_waves_per_eu(1, 1))) void bwd_dq_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[2 * kQStageBytes];
+  __shared__ int s_range[8];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, h = lane >> 5;
+  const int kvh = blockIdx.x % p.hkv;
+  const int t = blockIdx.x / p.hkv;
+  const int b = t < p.items[0] ? 0 : 1;
+  // Latest positions first in each branch (longest rows first).
+  const int item = b == 0 ? p.items[0] - 1 - t : p.items[0] + p.items[1] - 1 - t;
+  const int blk = item * (kRowsPerItem / kBRows) + wave;
+  const bool blk_ok = blk < p.blocks[b];
+  const int64_t pb = packed_block(p, b, kvh, blk_ok ? blk : 0);
+  const int r = blk * kBRows + n;
+  const bool valid = blk_ok && r < p.nrows[b];
+
+  float lse = 0.f, delta = 0.f;
+  int ks = 0, ke = 0;
+  bf16x8 qf[8], dof[8];
+  if (valid) {
+    const float* inf = reinterpret_cast<const float*>(p.info + pb * kInfoBytes);
+    const int* infi = reinterpret_cast<const int*>(inf);
+    lse = inf[kInfoLse + n];
+    delta = inf[kInfoDelta + n];
+    ks = infi[kInfoStart + n];
+    ke = infi[kInfoEnd + n];
+    const uint16_t* qrow = p.qp + pb * (kBlockBytes / 2) + n * kD + 8 * h;
+    const uint16_t* drow = p.dop + pb * (kBlockBytes / 2) + n * kD + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
+      dof[kk] = *reinterpret_cast<const bf16x8*>(drow + 16 * kk);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = dof[kk] = bf16x8{};
+  }
+  const bool has = valid && ks < ke;
+  const int w_min_s = wave_min(has ? ks : INT_MAX);
+  const int w_max_e = wave_max(has ? ke : INT_MIN);
+  if (lane == 0) {
+    s_range[wave] = w_min_s;
+    s_range[4 + wave] = w_max_e;
+  }
+  __syncthreads();
+  int g_s = INT_MAX, g_e = INT_MIN;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    g_s = min(g_s, s_range[i]);
+    g_e = max(g_e, s_range[4 + i]);
+  }
+  const int t_begin = g_e > g_s ? g_s / kBN : 0;
+  const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
+  // Tiles inside the range of every row this wave stores need no mask.  A
+  // stored row with no key (start = end = 0) must see every tile masked, so
+  // it counts as start = +inf, end = -inf; lanes that store nothing do not
+  // count (their columns of the products are independent and discarded).
+  const int w_max_s = __builtin_amdgcn_readfirstlane(
+      wave_max(valid ? (has ? ks : INT_MAX) : INT_MIN));
+  const int w_min_e = __builtin_amdgcn_readfirstlane(
+      wave_min(valid ? (has ? ke : INT_MIN) : INT_MAX));
+  const int it0 = w_max_s > INT_MAX - kBN ? INT_MAX : (w_max_s + kBN - 1) / kBN;
+  const int it1 = w_min_e <= 0 ? 0 : w_min_e / kBN;
+
+  int koff[8], voff[4];
+  {
+    const int kx = h ^ swz(n);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) koff[kk] = n * kRowBytes + (((2 * kk) ^ kx) << 4);
+    const int vx = h ^ vswz(n);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) voff[s2] = n * kVtRowBytes + (((2 * s2) ^ vx) << 4);
+  }
+  const DqPlan pl = make_dq_plan(p, kvh, wave, lane);
+  const uint32_t lds0 = lds_addr(smem);
+  f32x16 dqt[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) dqt[d] = f32x16{};
+
+  if (t_end > t_begin) stage_dq(p, pl, kvh, t_begin, lds0);
+  for (int j = t_begin; j < t_end; ++j) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const int par = (j - t_begin) & 1;
+    if (j + 1 < t_end) stage_dq(p, pl, kvh, j + 1, lds0 + (par ^ 1) * kQStageBytes);
+    const int key0 = j * kBN;
+    if (!(key0 < w_max_e && key0 + kBN > w_min_s)) continue;
+    const char* sk = smem + par * kQStageBytes;
+    const char* sv = sk + kTileBytes;
+    const char* st = sk + 2 * kTileBytes;
+    f32x16 s0 = f32x16{}, s1 = f32x16{}, p0 = f32x16{}, p1 = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sk + koff[kk]);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sk + koff[kk] + 32 * kRowBytes);
+      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(sv + koff[kk]);
+      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(sv + koff[kk] + 32 * kRowBytes);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk], s1, 0, 0, 0);
+      p0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b0, dof[kk], p0, 0, 0, 0);
+      p1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(b1, dof[kk], p1, 0, 0, 0);
+    }
+    // Element 4j+i of block kb is key key0 + 32kb + 8j + 4h + i of this row.
+    if (j < it0 || j >= it1) {
+      const int lo = ks - key0 - 4 * h, hi = ke - key0 - 4 * h;
+      const uint32_t span = hi > lo ? static_cast<uint32_t>(hi - lo) : 0u;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 8 * jj + i;
+          if (static_cast<uint32_t>(e - lo) >= span) s0[4 * jj + i] = -INFINITY;
+          if (static_cast<uint32_t>(e + 32 - lo) >= span) s1[4 * jj + i] = -INFINITY;
+        }
+      }
+    }
+    bf16x8 dsk[4];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pa = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[e], p.c, -lse));
+      const float pc = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[e], p.c, -lse));
+      dsk[e >> 3][e & 7] = static_cast<__bf16>(pa * (p0[e] - delta));
+      dsk[2 + (e >> 3)][e & 7] = static_cast<__bf16>(pc * (p1[e] - delta));
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const bf16x8 at = *reinterpret_cast<const bf16x8*>(st + voff[s2] + 32 * d * kVtRowBytes);
+        dqt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at, dsk[s2], dqt[d], 0, 0, 0);
+      }
+    }
+  }
+
+  if (valid) {
+    const int G = p.group;
+    const int slot = r / G;
+    const int qh = kvh * G + (r - slot * G);
+    const int pos = p.idx[b][slot];
+    uint16_t* row = p.dq + (static_cast<int64_t>(pos) * p.hq + qh) * kD + 4 * h;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint2 u;
+        u.x = pack_bf16x2(dqt[d][4 * j + 0] * p.scale, dqt[d][4 * j + 1] * p.scale);
+        u.y = pack_bf16x2(dqt[d][4 * j + 2] * p.scale, dqt[d][4 * j + 3] * p.scale);
+        *reinterpret_cast<uint2*>(row + 32 * d + 8 * j) = u;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+struct BwdLayout {
+  int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles128;
+  size_t off_info, off_qp, off_dop, off_qt, off_dot, off_kt, off_ranges, bytes;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, int64_t n_full,
+                            int64_t n_local) {
+  BwdLayout L{};
+  const int64_t n[2] = {n_full, n_local};
+  for (int b = 0; b < 2; ++b) {
+    L.blocks[b] = ceil_div(n[b] * group, kBRows);
+    L.items[b] = ceil_div(n[b] * group, kRowsPerItem);
+  }
+  L.total_blocks = static_cast<int64_t>(heads_kv) * (L.blocks[0] + L.blocks[1]);
+  L.kv_tiles = ceil_div(total_kv, kBN);
+  L.kv_tiles128 = ceil_div(total_kv, kKeysDkv);
+  size_t o = 0;
+  L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
+  L.off_qp = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
+  L.off_dop = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
+  L.off_qt = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
+  L.off_dot = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
+  L.off_kt = o;     o = align256(o + static_cast<size_t>(heads_kv) * L.kv_tiles * kTileBytes);
+  L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles128) * 2 * sizeof(int32_t));
+  L.bytes = o;
+  return L;
+}
+
+}  // namespace
+}  // namespace swattn
+
+using namespace swattn;
+using namespace swattn::tiles;
+
+extern "C" size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_kv,
+                                                     int32_t heads_q, int32_t heads_kv,
+                                                     int32_t head_dim, int64_t n_full,
+                                                     int64_t n_local) {
+  if (batch < 1 || seq_kv < 1 || heads_q < 1 || heads_kv < 1 || head_dim != kD ||
+      heads_q % heads_kv != 0 || n_full < 0 || n_local < 0)
+    return 0;
+  const BwdLayout L = bwd_layout(static_cast<int64_t>(batch) * seq_kv, heads_kv,
+                                 heads_q / heads_kv, n_full, n_local);
+  return L.bytes;
+}
+
+extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
+                                  const float* lse, const void* dout, const int32_t* full_idx,
+                                  int64_t n_full, const int32_t* local_idx, int64_t n_local,
+                                  const int32_t* full_starts, const int32_t* local_starts,
+                                  const int32_t* causal_ends, void* dq, void* dk, void* dv,
+                                  int32_t batch, int64_t seq_q, int64_t seq_kv, int32_t heads_q,
+                                  int32_t heads_kv, int32_t head_dim, int32_t window,
+                                  float scale_log2, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  if (head_dim != kD) return invalid("swattn_prefill_bwd: head_dim must be 128");
+  if (batch < 1 || seq_q < 0 || seq_kv < 1 || heads_q < 1 || heads_kv < 1)
+    return invalid("swattn_prefill_bwd: bad shape");
+  if (heads_q % heads_kv != 0)
+    return invalid("swattn_prefill_bwd: heads_q must be a multiple of heads_kv");
+  if (window <= 0) return invalid("swattn_prefill_bwd: window must be positive");
+  if (!(scale_log2 > 0.f) || !isfinite(scale_log2))
+    return invalid("swattn_prefill_bwd: scale_log2 must be positive and finite");
+  if (n_full < 0 || n_local < 0 || n_full + n_local > static_cast<int64_t>(batch) * seq_q)
+    return invalid("swattn_prefill_bwd: bad index counts");
+  const int64_t total_q = static_cast<int64_t>(batch) * seq_q;
+  const int64_t total_kv = static_cast<int64_t>(batch) * seq_kv;
+  if (total_q > INT32_MAX || total_kv > INT32_MAX - 2 * kKeysDkv)
+    return invalid("swattn_prefill_bwd: batch*seq must stay below 2^31");
+  const int64_t group = heads_q / heads_kv;
+  if ((n_full + n_local) * group > INT32_MAX - kRowsPerItem)
+    return invalid("swattn_prefill_bwd: too many rows");
+  const bool meta = full_starts != nullptr || local_starts != nullptr || causal_ends != nullptr;
+  if (meta && (full_starts == nullptr || local_starts == nullptr || causal_ends == nullptr))
+    return invalid("swattn_prefill_bwd: metadata needs full_starts, local_starts and causal_ends");
+  if (q == nullptr || k == nullptr || v == nullptr || dk == nullptr || dv == nullptr)
+    return invalid("swattn_prefill_bwd: null pointer");
+  if (n_full + n_local > 0 &&
+      (out == nullptr || lse == nullptr || dout == nullptr || dq == nullptr ||
+       (n_full > 0 && full_idx == nullptr) || (n_local > 0 && local_idx == nullptr)))
+    return invalid("swattn_prefill_bwd: null pointer");
+  const BwdLayout L = bwd_layout(total_kv, heads_kv, group, n_full, n_local);
+  if (workspace == nullptr || workspace_bytes < L.bytes) {
+    set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
+    return SWATTN_EWORKSPACE;
+  }
+  if (L.kv_tiles128 * heads_kv > INT32_MAX ||
+      (L.items[0] + L.items[1]) * heads_kv > INT32_MAX)
+    return invalid("swattn_prefill_bwd: grid too large");
+
+  char* ws = static_cast<char*>(workspace);
+  BwdParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.o = static_cast<const uint16_t*>(out);
+  p.dout = static_cast<const uint16_t*>(dout);
+  p.lse = lse;
+  p.dq = static_cast<uint16_t*>(dq);
+  p.dk = static_cast<uint16_t*>(dk);
+  p.dv = static_cast<uint16_t*>(dv);
+  p.idx[0] = full_idx;
+  p.idx[1] = local_idx;
+  p.starts[0] = full_starts;
+  p.starts[1] = local_starts;
+  p.ends = causal_ends;
+  p.count[0] = static_cast<int32_t>(n_full);
+  p.count[1] = static_cast<int32_t>(n_local);
+  for (int b = 0; b < 2; ++b) {
+    p.nrows[b] = static_cast<int32_t>(p.count[b] * group);
+    p.blocks[b] = static_cast<int32_t>(L.blocks[b]);
+    p.items[b] = static_cast<int32_t>(L.items[b]);
+  }
+  p.blk_base[0] = 0;
+  p.blk_base[1] = static_cast<int64_t>(heads_kv) * L.blocks[0];
+  p.info = ws + L.off_info;
+  p.qp = reinterpret_cast<uint16_t*>(ws + L.off_qp);
+  p.dop = reinterpret_cast<uint16_t*>(ws + L.off_dop);
+  p.qt = reinterpret_cast<uint16_t*>(ws + L.off_qt);
+  p.dot = reinterpret_cast<uint16_t*>(ws + L.off_dot);
+  p.kt = reinterpret_cast<uint16_t*>(ws + L.off_kt);
+  p.ranges = reinterpret_cast<int32_t*>(ws + L.off_ranges);
+  p.seq_q = static_cast<int32_t>(seq_q);
+  p.seq_kv = static_cast<int32_t>(seq_kv);
+  p.total_kv = static_cast<int32_t>(total_kv);
+  p.kv_tiles = static_cast<int32_t>(L.kv_tiles);
+  p.kv_tiles128 = static_cast<int32_t>(L.kv_tiles128);
+  p.hq = heads_q;
+  p.hkv = heads_kv;
+  p.group = static_cast<int32_t>(group);
+  p.window = window;
+  p.c = scale_log2;
+  p.scale = scale_log2 * 0.69314718055994531f;   // sm_scale = c * ln 2
+
+  const hipStream_t st = as_stream(stream);
+  const uint32_t rgrid = static_cast<uint32_t>(ceil_div(2 * L.kv_tiles128, kThreads));
+  if (meta)
+    hipLaunchKernelGGL(bwd_ranges_kernel<true>, dim3(rgrid), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL(bwd_ranges_kernel<false>, dim3(rgrid), dim3(kThreads), 0, st, p);
+  const int64_t nblk = L.blocks[0] + L.blocks[1];
+  if (nblk > 0) {
+    if (meta)
+      hipLaunchKernelGGL(bwd_prep_kernel<true>, dim3(static_cast<uint32_t>(nblk), heads_kv),
+                         dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL(bwd_prep_kernel<false>, dim3(static_cast<uint32_t>(nblk), heads_kv),
+                         dim3(kThreads), 0, st, p);
+  }
+  hipLaunchKernelGGL(vt_pack_kernel, dim3(p.kv_tiles, heads_kv), dim3(256), 0, st, p.k, p.kt,
+                     p.total_kv, heads_kv, p.kv_tiles);
+  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(L.kv_tiles128 * heads_kv)),
+                     dim3(kThreads), 0, st, p);
+  const int64_t qgrid = (L.items[0] + L.items[1]) * heads_kv;
+  if (qgrid > 0)
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(qgrid)), dim3(kThreads), 0, st, p);
+  return launch_status("swattn_prefill_bwd");
+}

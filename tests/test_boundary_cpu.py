@@ -34,7 +34,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     funcs = _header_functions()
-    assert len(funcs) == 13, funcs
+    assert len(funcs) == 16, funcs
     lib = _lib.lib()
     for name in funcs:
         assert hasattr(lib, name), name
@@ -52,6 +52,14 @@ def test_version_and_workspace():
     # V^T tiles: Hkv x ceil(B*Skv / 64) x 16 KiB
     assert lib.swattn_prefill_workspace_bytes(2, 100, 8, 128) == 8 * 4 * 16384
     assert lib.swattn_prefill_workspace_bytes(1, 100, 8, 64) == 0
+    # backward: per KV head and 32-row block 1 KiB of row info + four 8 KiB
+    # Q / dO blocks, K^T tiles, and 128-key block ranges (256-byte aligned).
+    nb = 8 * (-(-(300 * 4) // 32) + -(-(700 * 4) // 32))
+    kt = 8 * 16 * 16384
+    expect = nb * 1024 + 4 * nb * 8192 + kt + 256
+    assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 128, 300, 700) == expect
+    assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 30, 8, 128, 300, 700) == 0
+    assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 64, 300, 700) == 0
 
 
 def test_host_side_argument_errors():
@@ -82,6 +90,20 @@ def test_host_side_argument_errors():
                                      None) == -1
     assert lib.swattn_check_indices(None, -1, None, 0, 5, None, None) == -1
     assert lib.swattn_build_metadata(None, None, 1, 4, 4, 0, *([None] * 7), None) == -1
+    st = lib.swattn_prefill_bwd(*([dummy16] * 6), dummy16, 1, None, 0, None, None, None,
+                                *([dummy16] * 3), 1, 1, 1, 4, 4, 128, 4, ctypes.c_float(0.0),
+                                None, 0, None)
+    assert st == -1 and b"scale_log2" in lib.swattn_last_error()
+    st = lib.swattn_prefill_bwd(*([dummy16] * 6), dummy16, 1, None, 0, dummy16, None, None,
+                                *([dummy16] * 3), 1, 1, 1, 4, 4, 128, 4, ctypes.c_float(1.0),
+                                None, 0, None)
+    assert st == -1 and b"metadata" in lib.swattn_last_error()
+    st = lib.swattn_prefill_bwd(*([dummy16] * 6), dummy16, 1, None, 0, None, None, None,
+                                *([dummy16] * 3), 1, 1, 1, 4, 4, 128, 4, ctypes.c_float(1.0),
+                                None, 0, None)
+    assert st == -2 and b"workspace" in lib.swattn_last_error()
+    assert lib.swattn_mfma_peak(0, 1, dummy16, None) == -1
+    assert lib.swattn_mfma_peak(1, 1, None, None) == -1
 
 
 def test_api_rejects_cpu_and_dtype_errors_like_the_reference():

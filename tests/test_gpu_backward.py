@@ -1,0 +1,191 @@
+"""GPU parity of the routed prefill backward (dq, dk, dv) against the oracle.
+
+The reference is forward-only (V:14-15); the oracle's backward is the
+derivative of its pinned forward (see tests/test_oracle.py for its pins).
+
+Bar, per gradient tensor, against the fp32 oracle on the same bf16 inputs:
+* relative L2 error ||g - g_ref|| / ||g_ref|| <= 1e-2;
+* max-abs error <= 3e-2 * max|g_ref|.
+The kernel rounds P and dS to bf16 for the products and writes bf16 results
+(2^-9 relative each), and takes Delta = dO . O from the bf16 forward output;
+those errors are a few 1e-3 in both measures, and a wrong index, sign or
+dropped term gives errors of order 1.
+Full-size configs are checked on sampled rows (dq) plus the size-independent
+identities sum_j dk_j = 0 and sum_j dv_j = sum of the group's dO rows.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import routing as R
+from switchattentionkernels_amd import (
+    build_switch_attention_metadata,
+    build_switch_query_indices,
+    shard_attention_metadata,
+    switch_gqa_prefill,
+    switch_gqa_prefill_backward,
+    switch_gqa_prefill_forward,
+    workloads,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+REL_L2, REL_MAX = 1e-2, 3e-2
+
+
+def _qkv(seed, b, s, hq, hkv, skv=None):
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v = workloads.make_qkv(gen, b, s, s if skv is None else skv, hq, hkv, 128)
+    do = torch.randn(b, s, hq, 128, generator=gen).to(torch.bfloat16)
+    return q, k, v, do
+
+
+def _mask(seed, shape, p):
+    return torch.rand(shape, generator=torch.Generator().manual_seed(seed + 11)) < p
+
+
+def _grad_close(got, ref, tag, rows=None):
+    got = got.float().cpu()
+    ref = ref.float()
+    if rows is not None:
+        got, ref = got.reshape(-1, *got.shape[2:])[rows], ref.reshape(-1, *ref.shape[2:])[rows]
+    assert torch.isfinite(got).all(), f"{tag}: non-finite gradient"
+    err = got - ref
+    l2 = float(err.norm() / ref.norm().clamp_min(1e-20))
+    mx = float(err.abs().max() / ref.abs().max().clamp_min(1e-20))
+    print(f"[grad] {tag}: rel_l2 {l2:.2e} rel_max {mx:.2e}", flush=True)
+    assert l2 <= REL_L2 and mx <= REL_MAX, f"{tag}: rel_l2 {l2:.3e} rel_max {mx:.3e}"
+
+
+def _run(q, k, v, do, mask, window, metadata=None, md_np=None, sm_scale=None):
+    full, local = build_switch_query_indices(mask.to(DEV))
+    qd, kd, vd, dod = q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV)
+    o, lse = switch_gqa_prefill_forward(qd, kd, vd, full, local, window_size=window,
+                                        metadata=metadata, sm_scale=sm_scale)
+    dq, dk, dv = switch_gqa_prefill_backward(qd, kd, vd, o, lse, dod, full, local,
+                                             window_size=window, metadata=metadata,
+                                             sm_scale=sm_scale)
+    torch.cuda.synchronize()
+    return dq, dk, dv
+
+
+def _oracle(q, k, v, do, mask, window, md_np=None, rows=None, sm_scale=None):
+    full, local = R.compact(mask.numpy())
+    return oracle.routed_attention_backward(q, k, v, do, full, local, window_size=window,
+                                            metadata=md_np, rows=rows, sm_scale=sm_scale)
+
+
+def _md_np(md):
+    return {n: getattr(md, n).cpu().numpy() for n in ("full_starts", "local_starts",
+                                                      "causal_ends")}
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,skv", [
+    (1, 300, 8, 2, 64, 0.3, None),      # G = 4, ragged length
+    (2, 257, 4, 4, 100, 0.5, None),     # G = 1, two batch rows
+    (1, 520, 40, 8, 128, 0.25, None),   # G = 5: blocks straddle query positions
+    (1, 200, 64, 8, 1, 0.2, None),      # G = 8, window 1
+    (1, 1000, 32, 8, 1024, 0.25, None), # window beyond the sequence
+    (1, 384, 8, 2, 96, 0.0, None),      # all local
+    (1, 384, 8, 2, 96, 1.0, None),      # all full (dense causal)
+    (1, 300, 8, 2, 64, 0.4, 180),       # fewer keys than queries
+    (2, 200, 8, 2, 50, 0.3, 333),       # more keys than queries
+])
+def test_backward_matches_oracle(b, s, hq, hkv, w, p, skv):
+    q, k, v, do = _qkv(b * 1000 + s, b, s, hq, hkv, skv)
+    m = _mask(s + hq, (b, s), p)
+    dq, dk, dv = _run(q, k, v, do, m, w)
+    rq, rk, rv = _oracle(q, k, v, do, m, w)
+    tag = f"b{b} s{s} {hq}/{hkv} w{w} p{p} skv{skv}"
+    _grad_close(dq, rq, tag + " dq")
+    _grad_close(dk, rk, tag + " dk")
+    _grad_close(dv, rv, tag + " dv")
+
+
+def test_backward_custom_scale_and_determinism():
+    q, k, v, do = _qkv(5, 1, 400, 16, 4)
+    m = _mask(5, (1, 400), 0.3)
+    a = _run(q, k, v, do, m, 77, sm_scale=0.03)
+    bb = _run(q, k, v, do, m, 77, sm_scale=0.03)
+    for x, y in zip(a, bb):
+        assert torch.equal(x, y)   # no atomics: bit-identical reruns
+    ref = _oracle(q, k, v, do, m, 77, sm_scale=0.03)
+    for g, r, n in zip(a, ref, ("dq", "dk", "dv")):
+        _grad_close(g, r, "sm_scale=0.03 " + n)
+
+
+def test_backward_varlen_metadata():
+    cu = [0, 300, 301, 700, 1100]
+    q, k, v, do = _qkv(9, 1, 1100, 16, 4)
+    m = _mask(9, (1, 1100), 0.3)
+    md = build_switch_attention_metadata(1100, 1100, device=DEV, window_size=128, cu_seqlens=cu)
+    dq, dk, dv = _run(q, k, v, do, m, 128, metadata=md)
+    ref = _oracle(q, k, v, do, m, 128, md_np=_md_np(md))
+    for g, r, n in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        _grad_close(g, r, "varlen " + n)
+
+
+def test_backward_key_chunk_with_empty_rows():
+    """Query rows 512..767 of a 1024-token sequence against the key chunk
+    [600, 1000): rows before 600 see no key there (dq = 0) and keys no row
+    can see get dk = dv = 0."""
+    s, hq, hkv, w = 1024, 8, 2, 64
+    q, k, v, do = _qkv(13, 1, s, hq, hkv)
+    m = _mask(13, (1, s), 0.3)
+    rows = torch.arange(512, 768, dtype=torch.int32)
+    md = shard_attention_metadata(rows.to(DEV), kv_start=600, kv_end=1000, window_size=w)
+    qs, dos, ms = q[:, 512:768].contiguous(), do[:, 512:768].contiguous(), m[:, 512:768]
+    kc, vc = k[:, 600:1000].contiguous(), v[:, 600:1000].contiguous()
+    dq, dk, dv = _run(qs, kc, vc, dos, ms, w, metadata=md)
+    ref = _oracle(qs, kc, vc, dos, ms, w, md_np=_md_np(md))
+    assert torch.count_nonzero(dq[0, :600 - 512].float()) == 0
+    assert torch.count_nonzero(dk[0, 768 - 600:].float()) == 0
+    for g, r, n in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        _grad_close(g, r, "chunk " + n)
+
+
+def test_autograd_function_matches_backward():
+    q, k, v, do = _qkv(17, 1, 333, 8, 2)
+    m = _mask(17, (1, 333), 0.25)
+    full, local = build_switch_query_indices(m.to(DEV))
+    qd, kd, vd = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    out, lse = switch_gqa_prefill(qd, kd, vd, full, local, window_size=40)
+    assert not lse.requires_grad
+    (out.float() * do.to(DEV).float()).sum().backward()
+    dq, dk, dv = _run(q, k, v, do, m, 40)
+    assert torch.equal(qd.grad, dq) and torch.equal(kd.grad, dk) and torch.equal(vd.grad, dv)
+
+
+def test_b2_config_backward():
+    wl = workloads.build("b2", seed=3, p_full=0.25)
+    gen = torch.Generator().manual_seed(4)
+    do = torch.randn(wl["q"].shape, generator=gen).to(torch.bfloat16)
+    dq, dk, dv = _run(wl["q"], wl["k"], wl["v"], do, wl["mask"], wl["window"])
+    ref = _oracle(wl["q"], wl["k"], wl["v"], do, wl["mask"], wl["window"])
+    for g, r, n in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        _grad_close(g, r, "config b2 " + n)
+
+
+def test_s16k_backward_identities_and_sampled_rows():
+    wl = workloads.build("s16k", seed=0)
+    q, k, v, m, w = wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"]
+    gen = torch.Generator().manual_seed(5)
+    do = torch.randn(q.shape, generator=gen).to(torch.bfloat16)
+    dq, dk, dv = _run(q, k, v, do, m, w)
+    s, hq, hkv = q.shape[1], q.shape[2], k.shape[2]
+    g = hq // hkv
+    # sum_j dk_j = 0 per KV head (softmax is shift invariant in the keys),
+    # up to the bf16 rounding of each dk row.
+    dk32 = dk[0].float()
+    assert (dk32.sum(0).abs() <= 2e-3 * dk32.abs().sum(0) + 1e-3).all()
+    # sum_j dv_j = sum of dO over the group's query rows (rows of P sum to 1).
+    dv_sum = dv[0].float().sum(0).cpu()
+    ref = do[0].float().reshape(s, hkv, g, 128).sum((0, 2))
+    assert ((dv_sum - ref).abs() <= 2e-3 * do[0].float().abs().reshape(s, hkv, g, 128)
+            .sum((0, 2)) + 1e-2).all()
+    rows = np.unique(np.concatenate([np.random.default_rng(0).choice(s, 384, replace=False),
+                                     [0, 1, 1023, 1024, s - 1]]))
+    rq, _, _ = _oracle(q, k, v, do, m, w, rows=rows)
+    _grad_close(dq, rq, "s16k dq sampled rows", rows=torch.as_tensor(rows))

@@ -612,3 +612,14 @@ def test_decode_clamps_lengths_and_matches_prefill_last_row():
         o_p, lse_p, _, _ = _gpu_run(qs, k[i:i + 1, :n], v[i:i + 1, :n], mask, w)
         _assert_close(o[i:i + 1], lse[i:i + 1], o_p[:, n - 1:n].float().cpu(),
                       lse_p[:, n - 1:n].cpu(), tag=f"decode vs prefill row {i}")
+
+
+def test_mfma_probe_runs_and_is_deterministic():
+    """The roofline probe is a diagnostic: it must launch cleanly and
+    every workgroup (same operands) must produce the same finite sums."""
+    L = _lib.lib()
+    out = torch.empty(3 * 256, dtype=torch.float32, device=DEV)
+    assert L.swattn_mfma_peak(100, 3, out.data_ptr(), _lib.stream_handle(out.device)) == 0
+    r = out.view(3, 256).cpu()
+    assert torch.isfinite(r).all() and (r != 0).any()
+    assert torch.equal(r[0], r[1]) and torch.equal(r[0], r[2])

@@ -442,3 +442,117 @@ def test_decode_is_the_last_prefill_row():
     assert torch.isnan(o[0]).all() and torch.isneginf(lse[0]).all()
     o2, lse2 = A.decode_attention(q, k, v, [0, cache_len, 1, 1], [True] * 4, window_size=4)
     assert torch.equal(o[1], o2[1]) and torch.equal(lse[1], lse2[1])
+
+
+# ----------------------------------------------------------------------------
+# backward: the derivative of the forward restatement
+# ----------------------------------------------------------------------------
+
+def _loss_grad_fd(q, k, v, dout, mask, window, cu=None, h=1e-6):
+    """Central differences of L = sum(O * dO), O from the float64 brute force."""
+    q, k, v, dout = (np.array(x.numpy() if torch.is_tensor(x) else x, dtype=np.float64)
+                     for x in (q, k, v, dout))
+
+    def loss():
+        o, _ = A.brute_force_attention(q, k, v, mask, window, cu_seqlens=cu)
+        return float(np.nansum(o * dout))
+
+    grads = []
+    for x in (q, k, v):
+        gx = np.zeros_like(x)
+        it = np.nditer(x, flags=["multi_index"])
+        for _ in it:
+            i = it.multi_index
+            old = x[i]
+            x[i] = old + h
+            lp = loss()
+            x[i] = old - h
+            lm = loss()
+            x[i] = old
+            gx[i] = (lp - lm) / (2 * h)
+        grads.append(gx)
+    return grads
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,d,cu", [
+    (1, 7, 4, 2, 3, 0.5, 4, None),
+    (2, 5, 2, 1, 2, 0.4, 4, None),
+    (1, 8, 2, 2, 2, 0.5, 4, [0, 3, 8]),
+])
+def test_backward_matches_finite_differences_of_brute_force(b, s, hq, hkv, w, p, d, cu):
+    gen = torch.Generator().manual_seed(b * 31 + s)
+    q, k, v, do = (torch.randn(b, s, n, d, generator=gen, dtype=torch.float64)
+                   for n in (hq, hkv, hkv, hq))
+    m = _mask(s + 5, (b, s), p)
+    full, local = R.compact(m.numpy())
+    md = None if cu is None else R.varlen_metadata(cu, cu, w)
+    dq, dk, dv = A.routed_attention_backward(q, k, v, do, full, local, window_size=w,
+                                             metadata=md, dtype=torch.float64)
+    gq, gk, gv = _loss_grad_fd(q, k, v, do, m.numpy(), w, cu)
+    np.testing.assert_allclose(dq.numpy(), gq, atol=1e-7, rtol=1e-6)
+    np.testing.assert_allclose(dk.numpy(), gk, atol=1e-7, rtol=1e-6)
+    np.testing.assert_allclose(dv.numpy(), gv, atol=1e-7, rtol=1e-6)
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,meta", [
+    (1, 300, 8, 2, 64, 0.3, False),
+    (2, 130, 4, 4, 200, 0.5, False),
+    (1, 257, 5, 1, 17, 0.25, True),
+])
+def test_backward_matches_autograd_of_the_forward(b, s, hq, hkv, w, p, meta):
+    gen = torch.Generator().manual_seed(s)
+    q, k, v, do = (torch.randn(b, s, n, 32, generator=gen) for n in (hq, hkv, hkv, hq))
+    m = _mask(s, (b, s), p)
+    full, local = R.compact(m.numpy())
+    md = R.varlen_metadata([0, 100, 101, s], [0, 100, 101, s], w) if meta else None
+    qa, ka, va = (x.clone().requires_grad_(True) for x in (q, k, v))
+    o, _ = A.routed_attention(qa, ka, va, full, local, window_size=w, metadata=md, chunk=64)
+    (o * do).sum().backward()
+    dq, dk, dv = A.routed_attention_backward(q, k, v, do, full, local, window_size=w,
+                                             metadata=md, chunk=96)
+    for got, ref in ((dq, qa.grad), (dk, ka.grad), (dv, va.grad)):
+        torch.testing.assert_close(got, ref, atol=2e-5, rtol=1e-4)
+
+
+def test_backward_sum_invariants():
+    """sum_j dk_j = 0 (softmax is shift invariant in the keys) and
+    sum_j dv_j = sum over the group's rows of dO (each row of P sums to 1)."""
+    gen = torch.Generator().manual_seed(3)
+    b, s, hq, hkv = 2, 200, 8, 2
+    q, k, v, do = (torch.randn(b, s, n, 16, generator=gen) for n in (hq, hkv, hkv, hq))
+    full, local = R.compact(_mask(4, (b, s), 0.3).numpy())
+    _, dk, dv = A.routed_attention_backward(q, k, v, do, full, local, window_size=32)
+    for bb in range(b):
+        assert dk[bb].sum(0).abs().max() < 1e-4
+        ref = do[bb].reshape(s, hkv, hq // hkv, 16).sum((0, 2))
+        torch.testing.assert_close(dv[bb].sum(0), ref, atol=1e-3, rtol=1e-5)
+
+
+def test_backward_planted_mistakes_are_caught(monkeypatch):
+    def pins():
+        try:
+            test_backward_matches_finite_differences_of_brute_force(1, 7, 4, 2, 3, 0.5, 4, None)
+            test_backward_sum_invariants()
+        except AssertionError:
+            return False
+        return True
+
+    assert pins()
+    real = A._score_grad
+    monkeypatch.setattr(A, "_score_grad", lambda p, dp: p * dp)          # Delta dropped
+    assert not pins()
+    monkeypatch.setattr(A, "_score_grad", lambda p, dp: -real(p, dp))    # sign flipped
+    assert not pins()
+    monkeypatch.setattr(A, "_score_grad", real)
+    # GQA head mapping flipped in every product
+    real_bmm = torch.bmm
+
+    def swapped_bmm(a, b):
+        if a.dim() == 3 and a.shape[0] == 2 and b.shape[0] == 2:
+            b = b.flip(0)
+        return real_bmm(a, b)
+
+    monkeypatch.setattr(A.torch, "bmm", swapped_bmm)
+    assert not pins()
+    monkeypatch.setattr(A.torch, "bmm", real_bmm)
+    assert pins()
