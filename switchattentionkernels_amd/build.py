@@ -54,6 +54,10 @@ def compile_flags() -> list[str]:
         "-shared",
         # Keep the compiler from forming packed fp32 instructions.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in ordinary VGPRs: kernels whose registers exceed 256
+        # otherwise get every MFMA in the AGPR form, and the VALU then copies
+        # each score tile out of (and accumulators back into) AGPRs.
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         "-I", os.path.join(ROOT, "include"),
         "-I", CSRC,
     ]

@@ -49,15 +49,18 @@ namespace {
 
 using namespace tiles;
 
-constexpr int kThreads = 256;                          // four waves
+constexpr int kThreads = 256;                          // prep / ranges workgroups
+constexpr int kBwdWaves = 8;                           // dK/dV and dQ: two waves per SIMD
+constexpr int kBwdThreads = kBwdWaves * 64;
 constexpr int kBRows = 32;                             // rows per packed block
 constexpr int kBlockBytes = kBRows * kRowBytes;        // 8 KiB row-major or transposed block
 constexpr int kTRowBytes = kBRows * 2;                 // 64-byte transposed rows (one d, 32 rows)
 constexpr int kInfoBytes = 1024;                       // row info block
 constexpr int kInfoLse = 0, kInfoDelta = 32, kInfoStart = 64, kInfoEnd = 96;   // word offsets
 constexpr int kInfoMaxStart = 128, kInfoMinEnd = 129;
-constexpr int kKeysDkv = 128;                          // keys per dK/dV workgroup (32 per wave)
-constexpr int kRowsPerItem = 128;                      // rows per dQ workgroup (32 per wave)
+constexpr int kKeysDkv = kBwdWaves * 32;               // keys per dK/dV workgroup (32 per wave)
+constexpr int kRowsPerItem = kBwdWaves * 32;           // rows per dQ workgroup (32 per wave)
+constexpr int kVTileBytes = kKeysDkv * kRowBytes;      // the dK/dV workgroup's V rows: 64 KiB
 // dK/dV LDS stage: Q block, dO block, Q^T block, dO^T block, info.
 constexpr int kStageBytes = 4 * kBlockBytes + kInfoBytes;
 constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffQT = 2 * kBlockBytes, kOffDOT = 3 * kBlockBytes;
@@ -89,8 +92,8 @@ struct BwdParams {
   uint16_t* qt;              // [blocks][128 d][32 rows, perm16 in each 16-row group]
   uint16_t* dot;
   uint16_t* kt;              // K^T tiles [Hkv][kv_tiles][128][64]
-  int32_t* ranges;           // [2][kv_tiles128][2] block ranges
-  int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles128;
+  int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
+  int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
   float scale;               // sm_scale
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Block ranges: for each branch and 128-key tile, the packed blocks whose
+// Block ranges: for each branch and dK/dV key tile, the packed blocks whose
 // rows can see a key of the tile.  Row bounds are non-decreasing along each
 // list, so the slots that overlap [k0, k1) are [first with end > k0, first
 // with start >= k1).
@@ -238,8 +241,8 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
 template <bool kMeta>
 __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= 2 * p.kv_tiles128) return;
-  const int b = i / p.kv_tiles128, t = i - b * p.kv_tiles128;
+  if (i >= 2 * p.kv_tiles_dkv) return;
+  const int b = i / p.kv_tiles_dkv, t = i - b * p.kv_tiles_dkv;
   const int k0 = t * kKeysDkv, k1 = min(k0 + kKeysDkv, p.total_kv);
   const int n = p.count[b];
   int lo = 0, hi = n;
@@ -269,22 +272,26 @@ __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p)
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: one workgroup per (128-key tile, KV head).
+// dK / dV: one workgroup per (256-key tile, KV head), eight waves of 32 keys.
 // ---------------------------------------------------------------------------
 struct DkvPlan {
-  uint32_t off[8];   // this lane's source offset inside its wave's 8 KiB block, per 1 KiB load
+  uint32_t off[4];   // this lane's source offset inside its part, per 1 KiB load
+  uint32_t voff[8];  // V rows: source offset from the tile's first key row, per 1 KiB load
 };
 
-// Wave w stages block part w: 0 = Q, 1 = dO (row-major, 256-byte rows,
-// chunk swizzle swz), 2 = Q^T, 3 = dO^T (64-byte rows, swizzle tswz).  Lane l
-// of load i lands on byte 16 * (64 i + l) of the part and fetches the
-// logical chunk that belongs there.
-__device__ __forceinline__ DkvPlan make_dkv_plan(int wave, int lane) {
+// Waves 2p and 2p+1 stage the two halves of block part p: 0 = Q, 1 = dO
+// (row-major, 256-byte rows, chunk swizzle swz), 2 = Q^T, 3 = dO^T (64-byte
+// rows, swizzle tswz).  Lane l of load i lands on byte 16 * c of the part,
+// c = 256 half + 64 i + l, and fetches the logical chunk that belongs there.
+// The V tile (256 key rows, swizzle swz) is staged once: wave w loads rows
+// 32w .. 32w+31, four rows per load.
+__device__ __forceinline__ DkvPlan make_dkv_plan(const BwdParams& p, int kvh, int wave, int lane) {
   DkvPlan pl;
+  const int part = wave >> 1, half = wave & 1;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = 64 * i + lane;
-    if (wave < 2) {
+  for (int i = 0; i < 4; ++i) {
+    const int c = 256 * half + 64 * i + lane;
+    if (part < 2) {
       const int row = c >> 4;
       pl.off[i] = static_cast<uint32_t>(row * kRowBytes + (((c & 15) ^ swz(row)) << 4));
     } else {
@@ -292,25 +299,33 @@ __device__ __forceinline__ DkvPlan make_dkv_plan(int wave, int lane) {
       pl.off[i] = static_cast<uint32_t>(d * kTRowBytes + (((c & 3) ^ tswz(d)) << 4));
     }
   }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 32 * wave + 4 * i + (lane >> 4);
+    const int j = (lane & 15) ^ swz(row);
+    pl.voff[i] = static_cast<uint32_t>(((row * p.hkv + kvh) * kD + 8 * j) * 2);
+  }
   return pl;
 }
 
 __device__ __forceinline__ void stage_dkv(const BwdParams& p, const DkvPlan& pl, int wave,
                                           int lane, int64_t pb, uint32_t slot) {
-  const uint16_t* src = wave == 0 ? p.qp : wave == 1 ? p.dop : wave == 2 ? p.qt : p.dot;
+  const int part = wave >> 1, half = wave & 1;
+  const uint16_t* src = part == 0 ? p.qp : part == 1 ? p.dop : part == 2 ? p.qt : p.dot;
   const i32x4 rs = make_rsrc(src + pb * (kBlockBytes / 2), kBlockBytes);
-  const uint32_t dst = slot + wave * kBlockBytes;
+  const uint32_t dst = slot + part * kBlockBytes + half * (kBlockBytes / 2);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
-  if (wave == 0) {
+  for (int i = 0; i < 4; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
+  if (wave == kBwdWaves - 1) {
     const i32x4 ri = make_rsrc(p.info + pb * kInfoBytes, kInfoBytes);
     dma16(ri, static_cast<uint32_t>(16 * lane), __builtin_amdgcn_readfirstlane(slot + kOffInfo));
   }
 }
 
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void bwd_dkdv_kernel(const BwdParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kStageBytes];
+__global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
+                          amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_kernel(const BwdParams p) {
+  // [V tile: 256 key rows][two block slots]
+  __shared__ __attribute__((aligned(1024))) char smem[kVTileBytes + 2 * kStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -318,48 +333,60 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int kw0 = t * kKeysDkv + 32 * wave;   // this wave's first key
   const int key = kw0 + n;                    // this lane's key (B column)
 
-  // K and V of this lane's key as B operands: k-step kk holds d 16kk+8h .. +7.
-  bf16x8 kf[8], vf[8];
+  // K of this lane's key as B operands: k-step kk holds d 16kk+8h .. +7.
+  bf16x8 kf[8];
   if (key < p.total_kv) {
     const int64_t base = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      kf[kk] = *reinterpret_cast<const bf16x8*>(p.k + base + 16 * kk);
-      vf[kk] = *reinterpret_cast<const bf16x8*>(p.v + base + 16 * kk);
-    }
+    for (int kk = 0; kk < 8; ++kk) kf[kk] = *reinterpret_cast<const bf16x8*>(p.k + base + 16 * kk);
   } else {
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) kf[kk] = vf[kk] = bf16x8{};
+    for (int kk = 0; kk < 8; ++kk) kf[kk] = bf16x8{};
   }
   f32x16 dkt[4], dvt[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) dkt[d] = dvt[d] = f32x16{};
 
+  const int nt = p.kv_tiles_dkv;
   const int b0lo = p.ranges[2 * t], b0hi = p.ranges[2 * t + 1];
-  const int b1lo = p.ranges[2 * (p.kv_tiles128 + t)], b1hi = p.ranges[2 * (p.kv_tiles128 + t) + 1];
+  const int b1lo = p.ranges[2 * (nt + t)], b1hi = p.ranges[2 * (nt + t) + 1];
   const int n0 = max(b0hi - b0lo, 0), n1 = max(b1hi - b1lo, 0);
   const int nb = n0 + n1;
   auto block_of = [&](int i) -> int64_t {
     return i < n0 ? packed_block(p, 0, kvh, b0lo + i) : packed_block(p, 1, kvh, b1lo + i - n0);
   };
 
-  const DkvPlan pl = make_dkv_plan(wave, lane);
+  const DkvPlan pl = make_dkv_plan(p, kvh, wave, lane);
   const uint32_t lds0 = lds_addr(smem);
-  // Operand offsets: Q / dO rows (A of S, dP): row n, chunk 2kk + h;
-  // Q^T / dO^T rows (A of dK^T, dV^T): d row 32 dblk + n, chunk 2 s2 + h.
+  const uint32_t ring0 = lds0 + kVTileBytes;
+  // The V tile, once: rows past total_kv fall outside the descriptor.
+  if (nb > 0) {
+    const int64_t row_bytes = static_cast<int64_t>(p.hkv) * kD * 2;
+    const int64_t rest = (static_cast<int64_t>(p.total_kv) - static_cast<int64_t>(t) * kKeysDkv) * row_bytes;
+    const i32x4 rv = make_rsrc(reinterpret_cast<const char*>(p.v) + static_cast<int64_t>(t) * kKeysDkv * row_bytes,
+                               static_cast<uint32_t>(rest < 0xffffffffLL ? rest : 0xffffffffLL));
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      dma16(rv, pl.voff[i], __builtin_amdgcn_readfirstlane(lds0 + (32 * wave + 4 * i) * kRowBytes));
+  }
+  // Operand offsets: Q / dO rows (A of S, dP): row n, chunk 2kk + h; V rows
+  // (B of dP): key row 32 wave + n, chunk 2kk + h; Q^T / dO^T rows (A of
+  // dK^T, dV^T): d row 32 dblk + n, chunk 2 s2 + h.
   int aoff[8], toff[2];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) aoff[kk] = n * kRowBytes + (((2 * kk + h) ^ swz(n)) << 4);
 #pragma unroll
   for (int s2 = 0; s2 < 2; ++s2) toff[s2] = n * kTRowBytes + (((2 * s2 + h) ^ tswz(n)) << 4);
+  const char* vrow = smem + 32 * wave * kRowBytes;
 
-  if (nb > 0) stage_dkv(p, pl, wave, lane, block_of(0), lds0);
+  if (nb > 0) stage_dkv(p, pl, wave, lane, block_of(0), ring0);
   for (int i = 0; i < nb; ++i) {
-    // Block i is in LDS once every wave's loads are complete; every wave has
-    // finished block i-1, whose slot the next loads overwrite.
+    // Block i (and, before block 0, the V tile) is in LDS once every wave's
+    // loads are complete; every wave has finished block i-1, whose slot the
+    // next loads overwrite.
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (i + 1 < nb) stage_dkv(p, pl, wave, lane, block_of(i + 1), lds0 + ((i + 1) & 1) * kStageBytes);
-    const char* sb = smem + (i & 1) * kStageBytes;
+    if (i + 1 < nb) stage_dkv(p, pl, wave, lane, block_of(i + 1), ring0 + ((i + 1) & 1) * kStageBytes);
+    const char* sb = smem + kVTileBytes + (i & 1) * kStageBytes;
     const float* inf = reinterpret_cast<const float*>(sb + kOffInfo);
     const int* infi = reinterpret_cast<const int*>(inf);
 
@@ -368,8 +395,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
     for (int kk = 0; kk < 8; ++kk) {
       const bf16x8 aq = *reinterpret_cast<const bf16x8*>(sb + kOffQ + aoff[kk]);
       const bf16x8 ad = *reinterpret_cast<const bf16x8*>(sb + kOffDO + aoff[kk]);
+      const bf16x8 bv = *reinterpret_cast<const bf16x8*>(vrow + aoff[kk]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, kf[kk], s, 0, 0, 0);
-      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[kk], dp, 0, 0, 0);
+      dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, bv, dp, 0, 0, 0);
     }
     // Element e of the accumulators is row 8(e/4) + 4h + e%4 of the block.
     const bool interior = infi[kInfoMaxStart] <= kw0 && infi[kInfoMinEnd] >= kw0 + 32;
@@ -432,29 +460,30 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
 }
 
 // ---------------------------------------------------------------------------
-// dQ: one workgroup per (branch, 128-row tile, KV head).
+// dQ: one workgroup per (branch, 256-row tile, KV head), eight waves of 32 rows.
 // ---------------------------------------------------------------------------
+constexpr int kDqLoads = kBN / kBwdWaves / 4;   // 1 KiB loads per wave per K (V, K^T) tile
 struct DqPlan {
-  uint32_t koff[4];   // K / V row chunk offsets from the tile's first key row
-  uint32_t toff[4];   // K^T chunk offsets inside the K^T tile
-  uint32_t lds_w;     // this wave's byte offset inside a 16 KiB tile
+  uint32_t koff[kDqLoads];   // K / V row chunk offsets from the tile's first key row
+  uint32_t toff[kDqLoads];   // K^T chunk offsets inside the K^T tile
+  uint32_t lds_w;            // this wave's byte offset inside a 16 KiB tile
 };
 
-// Wave w stages key rows 16w .. 16w+15 of K and V and d rows 32w .. 32w+31
-// of K^T, 1 KiB (4 key rows / 8 d rows) per load; lane l lands on 16-byte
+// Wave w stages key rows 8w .. 8w+7 of K and V and d rows 16w .. 16w+15 of
+// K^T, 1 KiB (4 key rows / 8 d rows) per load; lane l lands on 16-byte
 // position l of the load and fetches the logical chunk that belongs there.
 __device__ __forceinline__ DqPlan make_dq_plan(const BwdParams& p, int kvh, int wave, int lane) {
   DqPlan pl;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * wave + 4 * i + (lane >> 4);
+  for (int i = 0; i < kDqLoads; ++i) {
+    const int row = 4 * kDqLoads * wave + 4 * i + (lane >> 4);
     const int j = (lane & 15) ^ swz(row);
     pl.koff[i] = static_cast<uint32_t>(((row * p.hkv + kvh) * kD + 8 * j) * 2);
-    const int d = 32 * wave + 8 * i + (lane >> 3);
+    const int d = 8 * kDqLoads * wave + 8 * i + (lane >> 3);
     const int jv = (lane & 7) ^ vswz(d);
     pl.toff[i] = static_cast<uint32_t>((d * kBN + 8 * jv) * 2);
   }
-  pl.lds_w = 16 * wave * kRowBytes;
+  pl.lds_w = 4 * kDqLoads * wave * kRowBytes;
   return pl;
 }
 
@@ -470,7 +499,7 @@ __device__ __forceinline__ void stage_dq(const BwdParams& p, const DqPlan& pl, i
                                  (static_cast<int64_t>(kvh) * p.kv_tiles + tk) * kTileBytes,
                              kTileBytes);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kDqLoads; ++i) {
     const uint32_t o = slot + pl.lds_w + 4 * i * kRowBytes;
     dma16(rk, pl.koff[i], __builtin_amdgcn_readfirstlane(o));
     dma16(rv, pl.koff[i], __builtin_amdgcn_readfirstlane(o + kTileBytes));
@@ -478,10 +507,10 @@ __device__ __forceinline__ void stage_dq(const BwdParams& p, const DqPlan& pl, i
   }
 }
 
-__global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
-                          amdgpu_waves_per_eu(1, 1))) void bwd_dq_kernel(const BwdParams p) {
+__global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
+                          amdgpu_waves_per_eu(2, 2))) void bwd_dq_kernel(const BwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[2 * kQStageBytes];
-  __shared__ int s_range[8];
+  __shared__ int s_range[2 * kBwdWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -522,14 +551,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int w_max_e = wave_max(has ? ke : INT_MIN);
   if (lane == 0) {
     s_range[wave] = w_min_s;
-    s_range[4 + wave] = w_max_e;
+    s_range[kBwdWaves + wave] = w_max_e;
   }
   __syncthreads();
   int g_s = INT_MAX, g_e = INT_MIN;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kBwdWaves; ++i) {
     g_s = min(g_s, s_range[i]);
-    g_e = max(g_e, s_range[4 + i]);
+    g_e = max(g_e, s_range[kBwdWaves + i]);
   }
   const int t_begin = g_e > g_s ? g_s / kBN : 0;
   const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
@@ -636,7 +665,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
 // Host side.
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles128;
+  int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles_dkv;
   size_t off_info, off_qp, off_dop, off_qt, off_dot, off_kt, off_ranges, bytes;
 };
 
@@ -652,7 +681,7 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   }
   L.total_blocks = static_cast<int64_t>(heads_kv) * (L.blocks[0] + L.blocks[1]);
   L.kv_tiles = ceil_div(total_kv, kBN);
-  L.kv_tiles128 = ceil_div(total_kv, kKeysDkv);
+  L.kv_tiles_dkv = ceil_div(total_kv, kKeysDkv);
   size_t o = 0;
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
   L.off_qp = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
@@ -660,7 +689,7 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   L.off_qt = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
   L.off_dot = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
   L.off_kt = o;     o = align256(o + static_cast<size_t>(heads_kv) * L.kv_tiles * kTileBytes);
-  L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles128) * 2 * sizeof(int32_t));
+  L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.bytes = o;
   return L;
 }
@@ -723,7 +752,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
     set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
     return SWATTN_EWORKSPACE;
   }
-  if (L.kv_tiles128 * heads_kv > INT32_MAX ||
+  if (L.kv_tiles_dkv * heads_kv > INT32_MAX ||
       (L.items[0] + L.items[1]) * heads_kv > INT32_MAX)
     return invalid("swattn_prefill_bwd: grid too large");
 
@@ -763,7 +792,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.seq_kv = static_cast<int32_t>(seq_kv);
   p.total_kv = static_cast<int32_t>(total_kv);
   p.kv_tiles = static_cast<int32_t>(L.kv_tiles);
-  p.kv_tiles128 = static_cast<int32_t>(L.kv_tiles128);
+  p.kv_tiles_dkv = static_cast<int32_t>(L.kv_tiles_dkv);
   p.hq = heads_q;
   p.hkv = heads_kv;
   p.group = static_cast<int32_t>(group);
@@ -772,7 +801,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.scale = scale_log2 * 0.69314718055994531f;   // sm_scale = c * ln 2
 
   const hipStream_t st = as_stream(stream);
-  const uint32_t rgrid = static_cast<uint32_t>(ceil_div(2 * L.kv_tiles128, kThreads));
+  const uint32_t rgrid = static_cast<uint32_t>(ceil_div(2 * L.kv_tiles_dkv, kThreads));
   if (meta)
     hipLaunchKernelGGL(bwd_ranges_kernel<true>, dim3(rgrid), dim3(kThreads), 0, st, p);
   else
@@ -788,10 +817,11 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   }
   hipLaunchKernelGGL(vt_pack_kernel, dim3(p.kv_tiles, heads_kv), dim3(256), 0, st, p.k, p.kt,
                      p.total_kv, heads_kv, p.kv_tiles);
-  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(L.kv_tiles128 * heads_kv)),
-                     dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(L.kv_tiles_dkv * heads_kv)),
+                     dim3(kBwdThreads), 0, st, p);
   const int64_t qgrid = (L.items[0] + L.items[1]) * heads_kv;
   if (qgrid > 0)
-    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(qgrid)), dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(qgrid)), dim3(kBwdThreads), 0, st,
+                       p);
   return launch_status("swattn_prefill_bwd");
 }
