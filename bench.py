@@ -23,8 +23,9 @@ The JSON line also carries:
   semantics -- the reference has no CPU path) on a bounded random row sample
   of the same workload, on this host's cores;
 * comparators: the same kernel on all-full routing (dense causal), torch
-  SDPA causal (flash backend) on the same shape, the compaction alone, and
-  the routed decode extension (64 sequences, 8192-key caches) against HBM.
+  SDPA causal (flash backend) on the same shape, the compaction alone, the
+  routed decode extension (64 sequences, 8192-key caches) against HBM, and
+  the routed backward (dq, dk, dv) of the same prefill.
 """
 
 from __future__ import annotations
@@ -226,6 +227,27 @@ def main():
     except Exception as exc:  # comparator only
         print(f"[bench] decode comparator unavailable: {exc}", file=sys.stderr, flush=True)
 
+    # ---- routed backward (extension): dq, dk, dv of the same prefill --------------
+    backward = None
+    try:
+        from switchattentionkernels_amd import switch_gqa_prefill_backward
+        gen = torch.Generator().manual_seed(args.seed + 1)
+        dout = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
+        o_f, lse_f = switch_gqa_prefill_forward(q, k, v, full, local, window_size=W)
+        bwd_ms = time_launches(lambda: switch_gqa_prefill_backward(q, k, v, o_f, lse_f, dout, full,
+                                                                   local, window_size=W),
+                               10, warmup=3)
+        # Five products per legal (row, key) pair (S, dP, dV, dK, dQ): 2.5x
+        # the forward's two; the dQ pass recomputes S and dP on top of that.
+        backward = {"ms": round(bwd_ms, 4), "tflops": round(2.5 * flops / (bwd_ms * 1e-3) / 1e12, 1),
+                    "flop_convention": "2.5 x routed forward FLOPs",
+                    "frac_of_peak": round(2.5 * flops / (bwd_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        print(f"[bench] backward {bwd_ms:.3f} ms ({backward['tflops']} TFLOP/s)", file=sys.stderr,
+              flush=True)
+        del dout, o_f, lse_f
+    except Exception as exc:  # comparator only
+        print(f"[bench] backward comparator unavailable: {exc}", file=sys.stderr, flush=True)
+
     # ---- traffic (committed rocprofv3 --pmc result, if any) ---------------------
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "fwd_s16k_p25_traffic.txt")
@@ -309,6 +331,7 @@ def main():
             "compaction_us": round(compact_ms * 1e3, 2),
             "compaction_gbs": round(compact_bytes / (compact_ms * 1e-3) / 1e9, 1),
             "decode": decode,
+            "backward": backward,
         },
     }
     print(json.dumps(res), flush=True)
