@@ -58,6 +58,8 @@ def parse():
     ap.add_argument("--no-sdpa", action="store_true", help="skip the torch SDPA comparator")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only loop the attention kernel (for rocprofv3 runs)")
+    ap.add_argument("--backward-only", action="store_true",
+                    help="only loop switch_gqa_prefill_backward (for rocprofv3 runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="with --kernel-only: also run 3 device copies of this many MiB "
                          "(calibrates the HBM byte counters)")
@@ -141,6 +143,19 @@ def main():
         print(json.dumps({"kernel_only": True, "launches": args.warmup + args.steps,
                           "timed_launches": args.steps, "entry_point_ms": round(kernel_ms, 4),
                           "calibration": calib}))
+        return
+
+    if args.backward_only:
+        from switchattentionkernels_amd import switch_gqa_prefill_backward
+        gen = torch.Generator().manual_seed(args.seed + 1)
+        dout = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
+        o_f, lse_f = switch_gqa_prefill_forward(q, k, v, full, local, window_size=W)
+        bwd_ms = time_launches(lambda: switch_gqa_prefill_backward(q, k, v, o_f, lse_f, dout, full,
+                                                                   local, window_size=W),
+                               args.steps, warmup=args.warmup)
+        print(json.dumps({"backward_only": True, "launches": args.warmup + args.steps,
+                          "timed_launches": args.steps, "entry_point_ms": round(bwd_ms, 4),
+                          "tflops_2p5x": round(2.5 * flops / (bwd_ms * 1e-3) / 1e12, 1)}))
         return
 
     # ---- timed region: K full steps -------------------------------------------
