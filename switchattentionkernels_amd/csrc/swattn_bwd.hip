@@ -54,17 +54,16 @@ constexpr int kBwdWaves = 8;                           // dK/dV and dQ: two wave
 constexpr int kBwdThreads = kBwdWaves * 64;
 constexpr int kBRows = 32;                             // rows per packed block
 constexpr int kBlockBytes = kBRows * kRowBytes;        // 8 KiB row-major or transposed block
-constexpr int kTRowBytes = kBRows * 2;                 // 64-byte transposed rows (one d, 32 rows)
 constexpr int kInfoBytes = 1024;                       // row info block
 constexpr int kInfoLse = 0, kInfoDelta = 32, kInfoStart = 64, kInfoEnd = 96;   // word offsets
 constexpr int kInfoMaxStart = 128, kInfoMinEnd = 129;
 constexpr int kKeysDkv = kBwdWaves * 32;               // keys per dK/dV workgroup (32 per wave)
 constexpr int kRowsPerItem = kBwdWaves * 32;           // rows per dQ workgroup (32 per wave)
 constexpr int kVTileBytes = kKeysDkv * kRowBytes;      // the dK/dV workgroup's V rows: 64 KiB
-// dK/dV LDS stage: Q block, dO block, Q^T block, dO^T block, info.
-constexpr int kStageBytes = 4 * kBlockBytes + kInfoBytes;
-constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffQT = 2 * kBlockBytes, kOffDOT = 3 * kBlockBytes;
-constexpr int kOffInfo = 4 * kBlockBytes;
+// dK/dV LDS ring slot: Q block, dO block (row-major), info; three slots.
+constexpr int kStageBytes = 2 * kBlockBytes + kInfoBytes;
+constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffInfo = 2 * kBlockBytes;
+constexpr int kRingSlots = 3;
 // dQ LDS stage: K tile, V tile, K^T tile (16 KiB each).
 constexpr int kQStageBytes = 3 * kTileBytes;
 
@@ -89,8 +88,6 @@ struct BwdParams {
   char* info;                // [blocks][1 KiB]
   uint16_t* qp;              // [blocks][32 rows][128]
   uint16_t* dop;
-  uint16_t* qt;              // [blocks][128 d][32 rows, perm16 in each 16-row group]
-  uint16_t* dot;
   uint16_t* kt;              // K^T tiles [Hkv][kv_tiles][128][64]
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
   int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles_dkv;
@@ -98,12 +95,6 @@ struct BwdParams {
   float c;                   // sm_scale * log2(e)
   float scale;               // sm_scale
 };
-
-// Transposed-block chunk swizzle: four 64-byte rows share a 256-byte bank
-// line, and (d >> 2) & 3 gives the four rows of each line position four
-// distinct chunks, so 16 lanes reading one chunk of 16 consecutive d rows
-// are conflict-free.
-__device__ __forceinline__ int tswz(int d) { return (d >> 2) & 3; }
 
 template <bool kMeta>
 __device__ __forceinline__ void row_bounds(const BwdParams& p, int branch, int pos, int& ks,
@@ -134,8 +125,6 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 // ---------------------------------------------------------------------------
 template <bool kMeta>
 __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
-  __shared__ uint16_t sq[kBRows][kD + 8];   // 272-byte rows
-  __shared__ uint16_t sdo[kBRows][kD + 8];
   __shared__ int s_ks[kBRows], s_ke[kBRows];
   const int x = blockIdx.x, kvh = blockIdx.y;
   const int b = x < p.blocks[0] ? 0 : 1;
@@ -187,8 +176,6 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
   for (int i = 0; i < 2; ++i) {
     *reinterpret_cast<uint4*>(qp + 8 * i) = qv[i];
     *reinterpret_cast<uint4*>(dop + 8 * i) = dv[i];
-    *reinterpret_cast<uint4*>(&sq[rr][16 * part + 8 * i]) = qv[i];
-    *reinterpret_cast<uint4*>(&sdo[rr][16 * part + 8 * i]) = dv[i];
   }
   if (part == 0) {
     float* inf = reinterpret_cast<float*>(p.info + pb * kInfoBytes);
@@ -201,25 +188,6 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
     s_ke[rr] = live ? ke : INT_MIN;
   }
   __syncthreads();
-  // Transposed blocks: row d holds the 32 rows' values of d; position t of
-  // each 16-row group holds row perm16(t) of the group.
-  uint16_t* qt = p.qt + pb * (kBlockBytes / 2);
-  uint16_t* dot = p.dot + pb * (kBlockBytes / 2);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int chunk = tid + kThreads * i;   // 128 d rows x 4 chunks of 8 positions
-    const int d = chunk >> 2, c = chunk & 3;
-    uint32_t wq[4], wd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int p0 = 8 * c + 2 * e;
-      const int r0 = (p0 & ~15) + perm16(p0 & 15), r1 = (p0 & ~15) + perm16((p0 + 1) & 15);
-      wq[e] = static_cast<uint32_t>(sq[r0][d]) | (static_cast<uint32_t>(sq[r1][d]) << 16);
-      wd[e] = static_cast<uint32_t>(sdo[r0][d]) | (static_cast<uint32_t>(sdo[r1][d]) << 16);
-    }
-    *reinterpret_cast<uint4*>(qt + d * kBRows + 8 * c) = make_uint4(wq[0], wq[1], wq[2], wq[3]);
-    *reinterpret_cast<uint4*>(dot + d * kBRows + 8 * c) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-  }
   if (tid == 0) {
     int ms = INT_MIN, me = INT_MAX;
     for (int i = 0; i < kBRows; ++i) {
@@ -275,29 +243,23 @@ __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p)
 // dK / dV: one workgroup per (256-key tile, KV head), eight waves of 32 keys.
 // ---------------------------------------------------------------------------
 struct DkvPlan {
-  uint32_t off[4];   // this lane's source offset inside its part, per 1 KiB load
+  uint32_t off[2];   // this lane's source offset inside its block part, per 1 KiB load
   uint32_t voff[8];  // V rows: source offset from the tile's first key row, per 1 KiB load
 };
 
-// Waves 2p and 2p+1 stage the two halves of block part p: 0 = Q, 1 = dO
-// (row-major, 256-byte rows, chunk swizzle swz), 2 = Q^T, 3 = dO^T (64-byte
-// rows, swizzle tswz).  Lane l of load i lands on byte 16 * c of the part,
-// c = 256 half + 64 i + l, and fetches the logical chunk that belongs there.
-// The V tile (256 key rows, swizzle swz) is staged once: wave w loads rows
-// 32w .. 32w+31, four rows per load.
+// Waves 4p .. 4p+3 stage the four quarters of block part p (0 = Q, 1 = dO;
+// row-major 256-byte rows, chunk swizzle swz): lane l of load i lands on
+// byte 16 c of the part, c = 128 quarter + 64 i + l, and fetches the logical
+// chunk that belongs there.  The V tile (256 key rows, swizzle swz) is
+// staged once: wave w loads rows 32w .. 32w+31, four rows per load.
 __device__ __forceinline__ DkvPlan make_dkv_plan(const BwdParams& p, int kvh, int wave, int lane) {
   DkvPlan pl;
-  const int part = wave >> 1, half = wave & 1;
+  const int quarter = wave & 3;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = 256 * half + 64 * i + lane;
-    if (part < 2) {
-      const int row = c >> 4;
-      pl.off[i] = static_cast<uint32_t>(row * kRowBytes + (((c & 15) ^ swz(row)) << 4));
-    } else {
-      const int d = c >> 2;
-      pl.off[i] = static_cast<uint32_t>(d * kTRowBytes + (((c & 3) ^ tswz(d)) << 4));
-    }
+  for (int i = 0; i < 2; ++i) {
+    const int c = 128 * quarter + 64 * i + lane;
+    const int row = c >> 4;
+    pl.off[i] = static_cast<uint32_t>(row * kRowBytes + (((c & 15) ^ swz(row)) << 4));
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -308,24 +270,46 @@ __device__ __forceinline__ DkvPlan make_dkv_plan(const BwdParams& p, int kvh, in
   return pl;
 }
 
+// Two 1 KiB loads per wave, plus the 1 KiB info block from the last wave.
 __device__ __forceinline__ void stage_dkv(const BwdParams& p, const DkvPlan& pl, int wave,
                                           int lane, int64_t pb, uint32_t slot) {
-  const int part = wave >> 1, half = wave & 1;
-  const uint16_t* src = part == 0 ? p.qp : part == 1 ? p.dop : part == 2 ? p.qt : p.dot;
+  const int part = wave >> 2, quarter = wave & 3;
+  const uint16_t* src = part == 0 ? p.qp : p.dop;
   const i32x4 rs = make_rsrc(src + pb * (kBlockBytes / 2), kBlockBytes);
-  const uint32_t dst = slot + part * kBlockBytes + half * (kBlockBytes / 2);
+  const uint32_t dst = slot + part * kBlockBytes + quarter * (kBlockBytes / 4);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
+  for (int i = 0; i < 2; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
   if (wave == kBwdWaves - 1) {
     const i32x4 ri = make_rsrc(p.info + pb * kInfoBytes, kInfoBytes);
     dma16(ri, static_cast<uint32_t>(16 * lane), __builtin_amdgcn_readfirstlane(slot + kOffInfo));
   }
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// A operand of X^T (32 d rows x 16 block rows, k-step s) read from the
+// row-major block X in LDS with two transposing reads (ds_read_b64_tr_b16).
+// In each 16-lane group, output lane i, element j of a read is element i%4
+// of the 8 bytes that lane 4j + i/4 of the group addressed.  Lane 4j + q of
+// group g = 2h + dh addresses row 16s + 8a + 4h + j, d = dbase + 16dh + 4q
+// (read a = 0, 1), so output lane (m = 16dh + i, h) holds X[row][dbase + m]
+// for the rows 16s + 8(t/4) + 4h + t%4, t = 0..7: the perm16 order in which
+// the S / dP accumulators hold the same rows as B operands.  toff[s][a] is
+// that address for dbase = 0; d block dblk adds 64 ((dblk ^ j) & 3), the
+// high half of the row's chunk swizzle.
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+__device__ __forceinline__ bf16x8 read_xt(const char* xb, int off0, int off1) {
+  __attribute__((address_space(3))) char* base = (__attribute__((address_space(3))) char*)(xb);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + off1));
+  const i16x4 v[2] = {lo, hi};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
                           amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_kernel(const BwdParams p) {
-  // [V tile: 256 key rows][two block slots]
-  __shared__ __attribute__((aligned(1024))) char smem[kVTileBytes + 2 * kStageBytes];
+  // [V tile: 256 key rows][three block slots]
+  __shared__ __attribute__((aligned(1024))) char smem[kVTileBytes + kRingSlots * kStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, h = lane >> 5;
@@ -370,23 +354,45 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
       dma16(rv, pl.voff[i], __builtin_amdgcn_readfirstlane(lds0 + (32 * wave + 4 * i) * kRowBytes));
   }
   // Operand offsets: Q / dO rows (A of S, dP): row n, chunk 2kk + h; V rows
-  // (B of dP): key row 32 wave + n, chunk 2kk + h; Q^T / dO^T rows (A of
-  // dK^T, dV^T): d row 32 dblk + n, chunk 2 s2 + h.
+  // (B of dP): key row 32 wave + n, chunk 2kk + h; Q^T / dO^T (A of dK^T,
+  // dV^T): transposing reads, see read_xt.
   int aoff[8], toff[2];
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) aoff[kk] = n * kRowBytes + (((2 * kk + h) ^ swz(n)) << 4);
+  // Transposing reads for k-step 0 (k-step s adds 16 rows: 4096 bytes; the
+  // swizzle's (row >> 2) & 3 does not change with it).
+  const int tj = (lane >> 2) & 3, tq = lane & 3, tdh = (lane >> 4) & 1;
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) toff[s2] = n * kTRowBytes + (((2 * s2 + h) ^ tswz(n)) << 4);
+  for (int a = 0; a < 2; ++a) {
+    const int row = 8 * a + 4 * h + tj;
+    const int clo = 2 * tdh + (tq >> 1);
+    toff[a] = row * kRowBytes + ((clo ^ ((row >> 2) & 3)) << 4) + ((tq & 1) << 3);
+  }
   const char* vrow = smem + 32 * wave * kRowBytes;
 
+  // Three-slot ring: block i+2 loads while block i is computed.
   if (nb > 0) stage_dkv(p, pl, wave, lane, block_of(0), ring0);
+  if (nb > 1) stage_dkv(p, pl, wave, lane, block_of(1), ring0 + kStageBytes);
+  int slot = 0;
   for (int i = 0; i < nb; ++i) {
     // Block i (and, before block 0, the V tile) is in LDS once every wave's
-    // loads are complete; every wave has finished block i-1, whose slot the
-    // next loads overwrite.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    if (i + 1 < nb) stage_dkv(p, pl, wave, lane, block_of(i + 1), ring0 + ((i + 1) & 1) * kStageBytes);
-    const char* sb = smem + kVTileBytes + (i & 1) * kStageBytes;
+    // own loads up to it are complete (block i+1's may stay in flight: two
+    // loads, three for the last wave); every wave has finished block i-1,
+    // whose slot the next loads overwrite.
+    if (i + 1 < nb) {
+      if (wave == kBwdWaves - 1)
+        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (i + 2 < nb) {
+      const int s2slot = slot >= 1 ? slot - 1 : slot + 2;   // (i + 2) % 3
+      stage_dkv(p, pl, wave, lane, block_of(i + 2), ring0 + s2slot * kStageBytes);
+    }
+    const char* sb = smem + kVTileBytes + slot * kStageBytes;
+    slot = slot == kRingSlots - 1 ? 0 : slot + 1;
     const float* inf = reinterpret_cast<const float*>(sb + kOffInfo);
     const int* infi = reinterpret_cast<const int*>(inf);
 
@@ -431,9 +437,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     for (int s2 = 0; s2 < 2; ++s2) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const int o = toff[s2] + 32 * d * kTRowBytes;
-        const bf16x8 ado = *reinterpret_cast<const bf16x8*>(sb + kOffDOT + o);
-        const bf16x8 aqt = *reinterpret_cast<const bf16x8*>(sb + kOffQT + o);
+        const int dx = (((d ^ tj) & 3) << 6) + 16 * kRowBytes * s2;
+        const bf16x8 ado = read_xt(sb + kOffDO, toff[0] + dx, toff[1] + dx);
+        const bf16x8 aqt = read_xt(sb + kOffQ, toff[0] + dx, toff[1] + dx);
         dvt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ado, pk[s2], dvt[d], 0, 0, 0);
         dkt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aqt, dsk[s2], dkt[d], 0, 0, 0);
       }
@@ -666,7 +672,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // ---------------------------------------------------------------------------
 struct BwdLayout {
   int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles_dkv;
-  size_t off_info, off_qp, off_dop, off_qt, off_dot, off_kt, off_ranges, bytes;
+  size_t off_info, off_qp, off_dop, off_kt, off_ranges, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -686,8 +692,6 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
   L.off_qp = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
   L.off_dop = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
-  L.off_qt = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
-  L.off_dot = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
   L.off_kt = o;     o = align256(o + static_cast<size_t>(heads_kv) * L.kv_tiles * kTileBytes);
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.bytes = o;
@@ -784,8 +788,6 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.info = ws + L.off_info;
   p.qp = reinterpret_cast<uint16_t*>(ws + L.off_qp);
   p.dop = reinterpret_cast<uint16_t*>(ws + L.off_dop);
-  p.qt = reinterpret_cast<uint16_t*>(ws + L.off_qt);
-  p.dot = reinterpret_cast<uint16_t*>(ws + L.off_dot);
   p.kt = reinterpret_cast<uint16_t*>(ws + L.off_kt);
   p.ranges = reinterpret_cast<int32_t*>(ws + L.off_ranges);
   p.seq_q = static_cast<int32_t>(seq_q);
