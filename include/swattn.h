@@ -201,7 +201,9 @@ int swattn_merge_partials(const void* const* o_parts, const float* const* lse_pa
  *            V:236-241); a sequence with no key gets O = NaN, LSE = -inf.
  *   heads_q / heads_kv <= 8.  workspace >= swattn_decode_workspace_bytes(),
  *   which depends on the current device's CU count (ask on that device).
- * Split-K over 256-key chunks, fp32 partials merged in a second kernel.
+ * A one-workgroup plan kernel sizes key chunks on the device from the routed
+ * key total (at least 256 keys, the same size for full and local
+ * sequences); one workgroup per chunk; fp32 partials merged by a third kernel.
  */
 size_t swattn_decode_workspace_bytes(int32_t batch, int64_t cache_len, int32_t heads_q,
                                      int32_t heads_kv);

@@ -5,10 +5,14 @@
 // [p - window + 1, p] when local).  The reference has no decode path.
 //
 // HBM-bound: every cached key and value of the routed range is read once per
-// KV head.  Split-K (a few workgroups per sequence and KV head, each
-// streaming a long key range with an online softmax) keeps the chip busy for
-// one long sequence as well as for many short ones; a second kernel merges
-// the fp32 split partials in the log2 domain (LSE as V:236-241).
+// KV head.  Split-K (workgroups each streaming one chunk of one sequence's
+// routed keys with an online softmax) keeps the chip busy for one long
+// sequence as well as for many short ones.  Which keys are routed is known
+// only on the device, so a one-workgroup plan kernel sums the routed key
+// counts, picks one chunk size for the whole launch, and writes the list of
+// (sequence, KV head, chunk) work items: full and local sequences then get
+// chunks of the same size, whatever the mix.  A third kernel merges the
+// fp32 split partials in the log2 domain (LSE as V:236-241).
 //
 // Layout: q [B, Hq, 128], caches [B, L, Hkv, 128] bf16; out [B, Hq, 128] bf16,
 // lse [B, Hq] fp32.  Group size G = Hq / Hkv <= 8.
@@ -33,13 +37,16 @@ struct DecodeParams {
   const uint16_t* v;
   const int32_t* lens;
   const uint8_t* full;
-  float* part_o;     // [B][Hkv][nch][G][128] unnormalised sum of p * v, per split
-  float* part_ml;    // [B][Hkv][nch][G][2]   split max (exp2 domain) and sum of p
+  float* part_o;     // [split][G][128] unnormalised sum of p * v, per work item
+  float* part_ml;    // [split][G][2]   split max (exp2 domain) and sum of p
+  int2* items;       // [split] (pair = b * Hkv + kvh, chunk index)   (plan output)
+  int64_t* plan;     // [0] chunk keys, [1] work items; [2 + 2b] first item of b, [3 + 2b] chunks of b
   uint16_t* out;
   float* lse;
   int64_t cache_len; // L
-  int hq, hkv, group, nch, window;
-  int64_t span;      // keys per split (a multiple of 16)
+  int batch, hq, hkv, group, window;
+  int max_items;     // grid size of the split kernel (an upper bound on the work items)
+  int target;        // work items the chunk size aims at
   float c;           // sm_scale * log2(e)
 };
 
@@ -65,8 +72,85 @@ __device__ __forceinline__ void key_range(const DecodeParams& p, int b, int64_t&
   lo = p.full[b] ? 0 : (len - p.window > 0 ? len - p.window : 0);
 }
 
-// One workgroup per (split, KV head, sequence); the split covers `span` keys
-// from split * span.  Lane l works on the keys of key group kg = l / 16 and on
+// Plan: one workgroup of 1024 threads.  T = total routed keys over all
+// (sequence, KV head) pairs; chunk = max(256, ceil(T / target),
+// ceil(L / 256)) rounded up to 16, so that there are at most target + pairs
+// work items and at most 256 per pair; sequence b gets ceil(keys_b / chunk)
+// chunks per KV head.  Work items are numbered sequence by sequence, KV head
+// by KV head, chunk by chunk.
+constexpr int kPlanThreads = 1024;
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
+  __shared__ int64_t s_red[kPlanThreads / 64];
+  __shared__ int64_t s_scan[kPlanThreads];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (p.batch + kPlanThreads - 1) / kPlanThreads;
+  const int b0 = min(tid * per, p.batch), b1 = min(b0 + per, p.batch);
+  int64_t keys = 0;
+  for (int b = b0; b < b1; ++b) {
+    int64_t lo, hi;
+    key_range(p, b, lo, hi);
+    keys += hi - lo;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) keys += __shfl_xor(keys, off);
+  if (lane == 0) s_red[wave] = keys;
+  __syncthreads();
+  int64_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) total += s_red[w];
+  total *= p.hkv;
+  int64_t chunk = (total + p.target - 1) / p.target;
+  const int64_t by_len = (p.cache_len + 255) / 256;
+  chunk = chunk > by_len ? chunk : by_len;
+  chunk = chunk > 256 ? chunk : 256;
+  chunk = (chunk + 15) & ~static_cast<int64_t>(15);
+  int64_t cnt = 0;
+  for (int b = b0; b < b1; ++b) {
+    int64_t lo, hi;
+    key_range(p, b, lo, hi);
+    cnt += (hi - lo + chunk - 1) / chunk;
+  }
+  // Inclusive scan of the per-thread chunk counts (Hillis-Steele in LDS).
+  s_scan[tid] = cnt;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int64_t add = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += add;
+    __syncthreads();
+  }
+  int64_t run = s_scan[tid] - cnt;   // chunks (per KV head) before sequence b0
+  for (int b = b0; b < b1; ++b) {
+    int64_t lo, hi;
+    key_range(p, b, lo, hi);
+    const int64_t n = (hi - lo + chunk - 1) / chunk;
+    p.plan[2 + 2 * b] = run * p.hkv;
+    p.plan[3 + 2 * b] = n;
+    run += n;
+  }
+  const int64_t items = s_scan[kPlanThreads - 1] * p.hkv;
+  if (tid == 0) {
+    p.plan[0] = chunk;
+    p.plan[1] = items;
+  }
+  __syncthreads();   // every sequence's first item and chunk count are written
+  // Work items, one per thread at a time: item i belongs to the last
+  // sequence whose first item is <= i (sequences without keys own none).
+  for (int64_t i = tid; i < items; i += kPlanThreads) {
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (p.plan[2 + 2 * mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    const int64_t r = i - p.plan[2 + 2 * lo];
+    const int64_t n = p.plan[3 + 2 * lo];
+    const int kvh = static_cast<int>(r / n);
+    p.items[i] = make_int2(lo * p.hkv + kvh, static_cast<int>(r - static_cast<int64_t>(kvh) * n));
+  }
+}
+
+// One workgroup per work item (a chunk of `chunk` keys of one sequence's
+// routed range, for one KV head).  Lane l works on the keys of key group kg = l / 16 and on
 // dims 8*(l%16) .. +7: wave w takes the keys 16*i + 4*w + kg of its split, so
 // the four waves sweep the split together, four keys per wave per step.
 // Each key group keeps its own online-softmax state (running max m, sum l,
@@ -78,15 +162,17 @@ template <int G>
 __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
   __shared__ float s_m[kDecWaves][G], s_l[kDecWaves][G];
   __shared__ float s_acc[kDecWaves][G][kD];
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int64_t slot = blockIdx.x;
+  if (slot >= p.plan[1]) return;   // beyond the planned work items
+  const int2 item = p.items[slot];
+  const int b = item.x / p.hkv, kvh = item.x - (item.x / p.hkv) * p.hkv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int kg = lane >> 4, ds = lane & 15;
   int64_t lo, hi;
   key_range(p, b, lo, hi);
-  const int64_t s0 = static_cast<int64_t>(split) * p.span;
-  const int64_t k0 = s0 > lo ? s0 : lo;
-  const int64_t k1 = s0 + p.span < hi ? s0 + p.span : hi;
-  const int64_t slot = (static_cast<int64_t>(b) * p.hkv + kvh) * p.nch + split;
+  const int64_t chunk = p.plan[0];
+  const int64_t k0 = lo + static_cast<int64_t>(item.y) * chunk;
+  const int64_t k1 = k0 + chunk < hi ? k0 + chunk : hi;
   float* po = p.part_o + slot * G * kD;
   float* pml = p.part_ml + slot * G * 2;
   if (k0 >= k1) {   // no key of this sequence in the split: an empty partial
@@ -248,10 +334,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = static_cast<int>(row / p.hq), hq = static_cast<int>(row - static_cast<int64_t>(b) * p.hq);
   const int kvh = hq / p.group, h = hq - kvh * p.group;
-  const int64_t slot0 = (static_cast<int64_t>(b) * p.hkv + kvh) * p.nch;
+  const int nch = static_cast<int>(p.plan[3 + 2 * b]);   // at most 256
+  const int64_t slot0 = p.plan[2 + 2 * b] + static_cast<int64_t>(kvh) * nch;
   // Maximum over the non-empty splits.
   float mx = -INFINITY;
-  for (int c = tid; c < p.nch; c += 256) {
+  for (int c = tid; c < nch; c += 256) {
     const float* ml = p.part_ml + ((slot0 + c) * p.group + h) * 2;
     if (ml[1] > 0.f) mx = fmaxf(mx, ml[0]);
   }
@@ -262,7 +349,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p)
   const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   // Split weights 2^(m_c - M) (0 for empty splits) and the weighted sum of l.
   float lsum = 0.f;
-  for (int c = tid; c < p.nch; c += 256) {
+  for (int c = tid; c < nch; c += 256) {
     const float* ml = p.part_ml + ((slot0 + c) * p.group + h) * 2;
     const float w = (ml[1] > 0.f && M != -INFINITY) ? __builtin_amdgcn_exp2f(ml[0] - M) : 0.f;
     s_w[c] = w;
@@ -279,14 +366,14 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p)
   const int64_t cstride = static_cast<int64_t>(p.group) * kD;
   float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int c = half;
-  for (; c + 14 < p.nch; c += 16) {
+  for (; c + 14 < nch; c += 16) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float w = s_w[c + 2 * u];
       if (w != 0.f) a[u] += w * base[(c + 2 * u) * cstride];
     }
   }
-  for (; c < p.nch; c += 2) {
+  for (; c < nch; c += 2) {
     const float w = s_w[c];
     if (w != 0.f) a[0] += w * base[c * cstride];
   }
@@ -301,8 +388,6 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p)
   }
 }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
 }  // namespace
 }  // namespace swattn
 
@@ -310,21 +395,13 @@ using namespace swattn;
 
 extern "C" {
 
-// Splits per (sequence, KV head): about four workgroups per CU over the
-// whole launch (the routing, and so which splits are empty, is only known on
-// the device), at most kMaxSplits, and at least 256 keys per split.
-constexpr int kMaxSplits = kMaxSplitsDev;
+// Work items the chunk size aims at: about four workgroups per CU.  The
+// split kernel's grid is that plus one per (sequence, KV head) pair, an
+// upper bound on the planned items (rounding each pair's chunk count up).
 #ifndef SWATTN_SPLIT_TARGET
 #define SWATTN_SPLIT_TARGET 4
 #endif
 constexpr int kSplitTarget = SWATTN_SPLIT_TARGET;   // workgroups per CU
-static int64_t decode_splits(int64_t pairs, int64_t cache_len, int cus) {
-  int64_t n = (kSplitTarget * static_cast<int64_t>(cus) + pairs - 1) / pairs;
-  const int64_t by_len = (cache_len + 255) / 256;
-  if (n > by_len) n = by_len;
-  if (n > kMaxSplits) n = kMaxSplits;
-  return n < 1 ? 1 : n;
-}
 
 static int decode_cus() {
   int dev = 0, n = 0;
@@ -334,12 +411,28 @@ static int decode_cus() {
   return n;
 }
 
+struct DecodeLayout {
+  int64_t target, max_items, off_ml, off_items, off_plan, bytes;   // byte offsets
+};
+
+static DecodeLayout decode_layout(int64_t batch, int64_t heads_q, int64_t heads_kv, int cus) {
+  DecodeLayout L{};
+  L.target = static_cast<int64_t>(kSplitTarget) * cus;
+  L.max_items = L.target + batch * heads_kv;
+  const int64_t group = heads_q / heads_kv;
+  auto al = [](int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); };
+  int64_t o = al(L.max_items * group * kD * 4);           // part_o
+  L.off_ml = o;    o = al(o + L.max_items * group * 2 * 4);
+  L.off_items = o; o = al(o + L.max_items * 8);
+  L.off_plan = o;  o = al(o + (2 + 2 * batch) * 8);
+  L.bytes = o;
+  return L;
+}
+
 size_t swattn_decode_workspace_bytes(int32_t batch, int64_t cache_len, int32_t heads_q,
                                      int32_t heads_kv) {
   if (batch < 1 || cache_len < 1 || heads_q < 1 || heads_kv < 1 || heads_q % heads_kv) return 0;
-  const int64_t pairs = static_cast<int64_t>(batch) * heads_kv;
-  const int64_t slots = pairs * decode_splits(pairs, cache_len, decode_cus()) * (heads_q / heads_kv);
-  return static_cast<size_t>(slots) * (kD + 2) * sizeof(float);
+  return static_cast<size_t>(decode_layout(batch, heads_q, heads_kv, decode_cus()).bytes);
 }
 
 int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
@@ -371,12 +464,16 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.v = static_cast<const uint16_t*>(v_cache);
   p.lens = cache_lens;
   p.full = full;
-  const int64_t pairs = static_cast<int64_t>(batch) * heads_kv;
-  p.nch = static_cast<int>(decode_splits(pairs, cache_len, decode_cus()));
-  p.span = ceil_div(ceil_div(cache_len, p.nch), 16) * 16;
-  const int64_t slots = pairs * p.nch * group;
-  p.part_o = static_cast<float*>(workspace);
-  p.part_ml = p.part_o + slots * kD;
+  const DecodeLayout L = decode_layout(batch, heads_q, heads_kv, decode_cus());
+  if (L.max_items > INT32_MAX) return invalid("swattn_decode_fwd: too many work items");
+  char* ws = static_cast<char*>(workspace);
+  p.part_o = reinterpret_cast<float*>(ws);
+  p.part_ml = reinterpret_cast<float*>(ws + L.off_ml);
+  p.items = reinterpret_cast<int2*>(ws + L.off_items);
+  p.plan = reinterpret_cast<int64_t*>(ws + L.off_plan);
+  p.max_items = static_cast<int>(L.max_items);
+  p.target = static_cast<int>(L.target);
+  p.batch = batch;
   p.out = static_cast<uint16_t*>(out);
   p.lse = lse;
   p.cache_len = cache_len;
@@ -386,8 +483,8 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.window = window;
   p.c = scale_log2;
   const hipStream_t st = as_stream(stream);
-  const dim3 grid(static_cast<uint32_t>(p.nch), static_cast<uint32_t>(heads_kv),
-                  static_cast<uint32_t>(batch));
+  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, st, p);
+  const dim3 grid(static_cast<uint32_t>(p.max_items));
   switch (group) {
     case 1: hipLaunchKernelGGL(decode_split_kernel<1>, grid, dim3(256), 0, st, p); break;
     case 2: hipLaunchKernelGGL(decode_split_kernel<2>, grid, dim3(256), 0, st, p); break;

@@ -586,6 +586,26 @@ def test_decode_matches_oracle(hq, hkv, w):
                   tag=f"decode {hq}/{hkv} W{w}")
 
 
+def test_decode_plan_with_long_mixed_caches():
+    """Enough routed keys that the device plan picks chunks above 256 keys and
+    splits every full sequence into many of them, next to one-chunk local
+    sequences and an empty one."""
+    gen = torch.Generator().manual_seed(77)
+    b, cache_len, hq, hkv, w = 24, 16384, 8, 4, 512
+    q = torch.randn(b, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    lens = torch.randint(1, cache_len + 1, (b,), generator=gen)
+    lens[3] = 0
+    lens[5] = cache_len
+    full = torch.rand(b, generator=gen) < 0.7
+    o, lse = switch_gqa_decode_forward(q.to(DEV), k.to(DEV), v.to(DEV),
+                                       lens.to(torch.int32).to(DEV), full.to(DEV), window_size=w)
+    o_r, lse_r = oracle.decode_attention(q, k, v, lens.tolist(), full.tolist(), window_size=w)
+    _assert_close(o.unsqueeze(1), lse.unsqueeze(1), o_r.unsqueeze(1), lse_r.unsqueeze(1),
+                  tag="decode long mixed")
+
+
 def test_decode_clamps_lengths_and_matches_prefill_last_row():
     gen = torch.Generator().manual_seed(31)
     hq, hkv, cache_len, w = 16, 4, 700, 100
