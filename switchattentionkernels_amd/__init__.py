@@ -21,6 +21,7 @@ from .backward import (  # noqa: F401
     SwitchGQAPrefillFunction,
     switch_gqa_prefill,
     switch_gqa_prefill_backward,
+    switch_gqa_prefill_varlen,
 )
 
 __all__ = [
@@ -36,5 +37,6 @@ __all__ = [
     "switch_gqa_decode_forward",
     "switch_gqa_prefill_backward",
     "switch_gqa_prefill",
+    "switch_gqa_prefill_varlen",
     "SwitchGQAPrefillFunction",
 ]

@@ -11,7 +11,10 @@ its log2 LSE (V:236-241):
 * ``switch_gqa_prefill(q, k, v, full_query_indices, local_query_indices, *,
   metadata=None, window_size=1024, sm_scale=None) -> (output, lse)``: the
   forward of ``switch_gqa_prefill_forward`` as a ``torch.autograd.Function``
-  whose output is differentiable in q, k and v (the LSE output is not).
+  whose output is differentiable in q, k and v (the LSE output is not);
+* ``switch_gqa_prefill_varlen(q, k, v, full_query_indices,
+  local_query_indices, cu_seqlens, *, cu_seqlens_kv=None, window_size=1024,
+  sm_scale=None)``: the same for packed sequences.
 """
 
 from __future__ import annotations
@@ -21,7 +24,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from .metadata import SwitchAttentionMetadata
+from .metadata import SwitchAttentionMetadata, build_switch_attention_metadata
 from .prefill import (LOG2E, MSG_META, _check_lists, _check_metadata, _validate_qkv,
                       switch_gqa_prefill_forward)
 
@@ -143,3 +146,17 @@ def switch_gqa_prefill(q, k, v, full_query_indices, local_query_indices, *,
     """``switch_gqa_prefill_forward`` with autograd support for q, k, v."""
     return SwitchGQAPrefillFunction.apply(q, k, v, full_query_indices, local_query_indices,
                                           metadata, window_size, sm_scale)
+
+
+def switch_gqa_prefill_varlen(q, k, v, full_query_indices, local_query_indices, cu_seqlens, *,
+                              cu_seqlens_kv=None, window_size: int = 1024,
+                              sm_scale: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``switch_gqa_prefill_varlen_forward`` with autograd support for q, k, v:
+    ``q``/``k``/``v`` are ``[1, T, H, 128]`` with the sequences concatenated
+    along T at offsets ``cu_seqlens``."""
+    _validate_qkv(q, k, v)
+    md = build_switch_attention_metadata(int(q.shape[1]), int(k.shape[1]), device=q.device,
+                                         window_size=window_size, cu_seqlens=cu_seqlens,
+                                         cu_seqlens_kv=cu_seqlens_kv)
+    return switch_gqa_prefill(q, k, v, full_query_indices, local_query_indices, metadata=md,
+                              window_size=window_size, sm_scale=sm_scale)

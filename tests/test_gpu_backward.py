@@ -27,8 +27,10 @@ from switchattentionkernels_amd import (
     switch_gqa_prefill,
     switch_gqa_prefill_backward,
     switch_gqa_prefill_forward,
+    switch_gqa_prefill_varlen,
     workloads,
 )
+from switchattentionkernels_amd.metadata import SwitchAttentionMetadata
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -156,6 +158,40 @@ def test_autograd_function_matches_backward():
     (out.float() * do.to(DEV).float()).sum().backward()
     dq, dk, dv = _run(q, k, v, do, m, 40)
     assert torch.equal(qd.grad, dq) and torch.equal(kd.grad, dk) and torch.equal(vd.grad, dv)
+
+
+def test_varlen_autograd_matches_oracle():
+    cu = [0, 200, 201, 640]
+    q, k, v, do = _qkv(21, 1, 640, 8, 2)
+    m = _mask(21, (1, 640), 0.3)
+    full, local = build_switch_query_indices(m.to(DEV))
+    qd, kd, vd = (x.to(DEV).requires_grad_(True) for x in (q, k, v))
+    out, _ = switch_gqa_prefill_varlen(qd, kd, vd, full, local, cu, window_size=64)
+    (out.float() * do.to(DEV).float()).sum().backward()
+    md = build_switch_attention_metadata(640, 640, device=DEV, window_size=64, cu_seqlens=cu)
+    ref = _oracle(q, k, v, do, m, 64, md_np=_md_np(md))
+    for g, r, n in zip((qd.grad, kd.grad, vd.grad), ref, ("dq", "dk", "dv")):
+        _grad_close(g, r, "varlen autograd " + n)
+
+
+def test_backward_rejects_non_monotone_metadata():
+    """The backward locates the rows that see a key block by binary search over
+    each list's bounds, so metadata whose bounds go down along a list is refused
+    (the forward accepts it)."""
+    s = 64
+    q, k, v, do = _qkv(23, 1, s, 4, 2)
+    m = torch.zeros(1, s, dtype=torch.bool)
+    md = build_switch_attention_metadata(s, s, device=DEV, window_size=16)
+    ends = md.causal_ends.clone()
+    ends[10] = 3   # row 10 now ends before row 9
+    bad = SwitchAttentionMetadata(md.q_positions, md.kv_positions, md.q_segment_ids,
+                                  md.kv_segment_ids, md.full_starts, md.local_starts, ends)
+    full, local = build_switch_query_indices(m.to(DEV))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = switch_gqa_prefill_forward(qd, kd, vd, full, local, window_size=16, metadata=bad)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        switch_gqa_prefill_backward(qd, kd, vd, o, lse, do.to(DEV), full, local, window_size=16,
+                                    metadata=bad)
 
 
 def test_b2_config_backward():
