@@ -64,8 +64,8 @@ constexpr int kVTileBytes = kKeysDkv * kRowBytes;      // the dK/dV workgroup's 
 constexpr int kStageBytes = 2 * kBlockBytes + kInfoBytes;
 constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffInfo = 2 * kBlockBytes;
 constexpr int kRingSlots = 3;
-// dQ LDS stage: K tile, V tile, K^T tile (16 KiB each).
-constexpr int kQStageBytes = 3 * kTileBytes;
+// dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
+constexpr int kQStageBytes = 2 * kTileBytes;
 
 struct BwdParams {
   const uint16_t* q;
@@ -88,7 +88,6 @@ struct BwdParams {
   char* info;                // [blocks][1 KiB]
   uint16_t* qp;              // [blocks][32 rows][128]
   uint16_t* dop;
-  uint16_t* kt;              // K^T tiles [Hkv][kv_tiles][128][64]
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
   int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
@@ -468,16 +467,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // ---------------------------------------------------------------------------
 // dQ: one workgroup per (branch, 256-row tile, KV head), eight waves of 32 rows.
 // ---------------------------------------------------------------------------
-constexpr int kDqLoads = kBN / kBwdWaves / 4;   // 1 KiB loads per wave per K (V, K^T) tile
+constexpr int kDqLoads = kBN / kBwdWaves / 4;   // 1 KiB loads per wave per K (or V) tile
 struct DqPlan {
   uint32_t koff[kDqLoads];   // K / V row chunk offsets from the tile's first key row
-  uint32_t toff[kDqLoads];   // K^T chunk offsets inside the K^T tile
   uint32_t lds_w;            // this wave's byte offset inside a 16 KiB tile
 };
 
-// Wave w stages key rows 8w .. 8w+7 of K and V and d rows 16w .. 16w+15 of
-// K^T, 1 KiB (4 key rows / 8 d rows) per load; lane l lands on 16-byte
-// position l of the load and fetches the logical chunk that belongs there.
+// Wave w stages key rows 8w .. 8w+7 of K and V, 1 KiB (4 key rows) per load;
+// lane l lands on 16-byte position l of the load and fetches the logical
+// chunk that belongs there (chunk swizzle swz).
 __device__ __forceinline__ DqPlan make_dq_plan(const BwdParams& p, int kvh, int wave, int lane) {
   DqPlan pl;
 #pragma unroll
@@ -485,9 +483,6 @@ __device__ __forceinline__ DqPlan make_dq_plan(const BwdParams& p, int kvh, int 
     const int row = 4 * kDqLoads * wave + 4 * i + (lane >> 4);
     const int j = (lane & 15) ^ swz(row);
     pl.koff[i] = static_cast<uint32_t>(((row * p.hkv + kvh) * kD + 8 * j) * 2);
-    const int d = 8 * kDqLoads * wave + 8 * i + (lane >> 3);
-    const int jv = (lane & 7) ^ vswz(d);
-    pl.toff[i] = static_cast<uint32_t>((d * kBN + 8 * jv) * 2);
   }
   pl.lds_w = 4 * kDqLoads * wave * kRowBytes;
   return pl;
@@ -501,21 +496,17 @@ __device__ __forceinline__ void stage_dq(const BwdParams& p, const DqPlan& pl, i
   const int64_t kv_off = static_cast<int64_t>(tk) * kBN * row_bytes;
   const i32x4 rk = make_rsrc(reinterpret_cast<const char*>(p.k) + kv_off, nrec);
   const i32x4 rv = make_rsrc(reinterpret_cast<const char*>(p.v) + kv_off, nrec);
-  const i32x4 rt = make_rsrc(reinterpret_cast<const char*>(p.kt) +
-                                 (static_cast<int64_t>(kvh) * p.kv_tiles + tk) * kTileBytes,
-                             kTileBytes);
 #pragma unroll
   for (int i = 0; i < kDqLoads; ++i) {
     const uint32_t o = slot + pl.lds_w + 4 * i * kRowBytes;
     dma16(rk, pl.koff[i], __builtin_amdgcn_readfirstlane(o));
     dma16(rv, pl.koff[i], __builtin_amdgcn_readfirstlane(o + kTileBytes));
-    dma16(rt, pl.toff[i], __builtin_amdgcn_readfirstlane(o + 2 * kTileBytes));
   }
 }
 
 __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
                           amdgpu_waves_per_eu(2, 2))) void bwd_dq_kernel(const BwdParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[2 * kQStageBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kRingSlots * kQStageBytes];
   __shared__ int s_range[2 * kBwdWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -579,14 +570,21 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   const int it0 = w_max_s > INT_MAX - kBN ? INT_MAX : (w_max_s + kBN - 1) / kBN;
   const int it1 = w_min_e <= 0 ? 0 : w_min_e / kBN;
 
-  int koff[8], voff[4];
+  // K / V rows (A of S^T, dP^T): key row n (+32), chunk 2kk + h.  K^T (A of
+  // dQ^T): transposing reads of the K tile, as read_xt describes (rows are
+  // keys; k-step s2 adds 16 key rows).
+  int koff[8], toff[2];
   {
     const int kx = h ^ swz(n);
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) koff[kk] = n * kRowBytes + (((2 * kk) ^ kx) << 4);
-    const int vx = h ^ vswz(n);
+  }
+  const int tj = (lane >> 2) & 3, tq = lane & 3, tdh = (lane >> 4) & 1;
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) voff[s2] = n * kVtRowBytes + (((2 * s2) ^ vx) << 4);
+  for (int a = 0; a < 2; ++a) {
+    const int row = 8 * a + 4 * h + tj;
+    const int clo = 2 * tdh + (tq >> 1);
+    toff[a] = row * kRowBytes + ((clo ^ ((row >> 2) & 3)) << 4) + ((tq & 1) << 3);
   }
   const DqPlan pl = make_dq_plan(p, kvh, wave, lane);
   const uint32_t lds0 = lds_addr(smem);
@@ -594,16 +592,28 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 #pragma unroll
   for (int d = 0; d < 4; ++d) dqt[d] = f32x16{};
 
+  // Three-slot ring: tile j+2 loads while tile j is computed.
   if (t_end > t_begin) stage_dq(p, pl, kvh, t_begin, lds0);
+  if (t_end > t_begin + 1) stage_dq(p, pl, kvh, t_begin + 1, lds0 + kQStageBytes);
+  int slot = 0;
   for (int j = t_begin; j < t_end; ++j) {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const int par = (j - t_begin) & 1;
-    if (j + 1 < t_end) stage_dq(p, pl, kvh, j + 1, lds0 + (par ^ 1) * kQStageBytes);
+    // Tile j is in LDS once every wave's loads up to it are complete (tile
+    // j+1's 2 kDqLoads loads may stay in flight); every wave has finished
+    // tile j-1, whose slot the next loads overwrite.
+    static_assert(kDqLoads == 2, "the wait below allows four loads in flight");
+    if (j + 1 < t_end)
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (j + 2 < t_end) {
+      const int s2slot = slot >= 1 ? slot - 1 : slot + 2;   // (j - t_begin + 2) % 3
+      stage_dq(p, pl, kvh, j + 2, lds0 + s2slot * kQStageBytes);
+    }
+    const char* sk = smem + slot * kQStageBytes;
+    slot = slot == kRingSlots - 1 ? 0 : slot + 1;
     const int key0 = j * kBN;
     if (!(key0 < w_max_e && key0 + kBN > w_min_s)) continue;
-    const char* sk = smem + par * kQStageBytes;
     const char* sv = sk + kTileBytes;
-    const char* st = sk + 2 * kTileBytes;
     f32x16 s0 = f32x16{}, s1 = f32x16{}, p0 = f32x16{}, p1 = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
@@ -642,7 +652,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const bf16x8 at = *reinterpret_cast<const bf16x8*>(st + voff[s2] + 32 * d * kVtRowBytes);
+        const int dx = (((d ^ tj) & 3) << 6) + 16 * kRowBytes * s2;
+        const bf16x8 at = read_xt(sk, toff[0] + dx, toff[1] + dx);
         dqt[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at, dsk[s2], dqt[d], 0, 0, 0);
       }
     }
@@ -672,7 +683,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // ---------------------------------------------------------------------------
 struct BwdLayout {
   int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles_dkv;
-  size_t off_info, off_qp, off_dop, off_kt, off_ranges, bytes;
+  size_t off_info, off_qp, off_dop, off_ranges, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -692,7 +703,6 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
   L.off_qp = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
   L.off_dop = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
-  L.off_kt = o;     o = align256(o + static_cast<size_t>(heads_kv) * L.kv_tiles * kTileBytes);
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.bytes = o;
   return L;
@@ -788,7 +798,6 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.info = ws + L.off_info;
   p.qp = reinterpret_cast<uint16_t*>(ws + L.off_qp);
   p.dop = reinterpret_cast<uint16_t*>(ws + L.off_dop);
-  p.kt = reinterpret_cast<uint16_t*>(ws + L.off_kt);
   p.ranges = reinterpret_cast<int32_t*>(ws + L.off_ranges);
   p.seq_q = static_cast<int32_t>(seq_q);
   p.seq_kv = static_cast<int32_t>(seq_kv);
@@ -817,8 +826,6 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
       hipLaunchKernelGGL(bwd_prep_kernel<false>, dim3(static_cast<uint32_t>(nblk), heads_kv),
                          dim3(kThreads), 0, st, p);
   }
-  hipLaunchKernelGGL(vt_pack_kernel, dim3(p.kv_tiles, heads_kv), dim3(256), 0, st, p.k, p.kt,
-                     p.total_kv, heads_kv, p.kv_tiles);
   hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(L.kv_tiles_dkv * heads_kv)),
                      dim3(kBwdThreads), 0, st, p);
   const int64_t qgrid = (L.items[0] + L.items[1]) * heads_kv;
