@@ -15,24 +15,27 @@
 // * Rows are packed as in the forward (compacted query slot, head of the
 //   group; head fastest), in blocks of 32.  bwd_prep_kernel computes Delta
 //   once per row and writes, per (branch, KV head, block), Q and dO as
-//   row-major 8 KiB blocks (A operands of S = Q K^T and dP = dO V^T) and as
-//   transposed 8 KiB blocks with the rows of each 16-row group in perm16
-//   order (A operands of dK^T = Q^T dS and dV^T = dO^T P, whose B operands
-//   are then the S / dP accumulators themselves), plus a 1 KiB block of row
-//   info (LSE, Delta, key bounds, and the block's bounds summary).
-// * bwd_dkdv_kernel: one workgroup per (128-key tile, KV head); each wave
-//   keeps its 32 keys' K and V as MFMA B operands in registers and dK^T,
-//   dV^T (128 d x 32 keys each) in accumulators, and streams the row blocks
-//   that can see the tile (a contiguous block range per branch, found by
-//   bwd_ranges_kernel with a binary search over the monotone row bounds)
-//   through a two-slot LDS ring filled by buffer_load ... lds.  Four MFMA
-//   products per block: S, dP, dV^T += dO^T P, dK^T += Q^T dS.
-// * bwd_dq_kernel: one workgroup per (128-row tile, KV head), the forward's
-//   shape: each wave owns 32 rows, keeps Q^T and dO^T as B operands, and
-//   streams K, V and K^T tiles (K^T packed like the forward's V^T) through a
-//   two-slot LDS ring.  Three products per 64-key tile: S^T = K Q^T,
-//   dP^T = V dO^T, dQ^T += K^T dS^T (dS^T as B operand straight from the
-//   accumulator, keys permuted within 16-key groups on both sides).
+//   row-major 8 KiB blocks plus a 1 KiB block of row info (LSE, Delta, key
+//   bounds, and the block's bounds summary).
+// * bwd_dkdv_kernel: one workgroup of eight waves (two per SIMD) per
+//   (256-key tile, KV head); each wave keeps its 32 keys' K as MFMA B
+//   operands in registers and dK^T, dV^T (128 d x 32 keys each) in
+//   accumulators; the workgroup's V rows sit in LDS.  It streams the row
+//   blocks that can see the tile (a contiguous block range per branch,
+//   found by bwd_ranges_kernel with a binary search over the monotone row
+//   bounds) through a three-slot LDS ring filled by buffer_load ... lds.
+//   Four MFMA products per block: S = Q K^T, dP = dO V^T, dV^T += dO^T P,
+//   dK^T += Q^T dS.  The A operands of the last two (Q^T, dO^T) come from
+//   the same row-major blocks through transposing LDS reads
+//   (ds_read_b64_tr_b16) that deliver the rows of each 16-row group in the
+//   order the S / dP accumulators hold them, so those accumulators are the
+//   B operands unchanged.
+// * bwd_dq_kernel: one workgroup of eight waves per (branch, 256-row tile,
+//   KV head), the forward's shape: each wave owns 32 rows, keeps Q^T and
+//   dO^T as B operands, and streams K and V tiles through a three-slot LDS
+//   ring.  Three products per 64-key tile: S^T = K Q^T, dP^T = V dO^T,
+//   dQ^T += K^T dS^T (K^T by transposing reads of the K tile; dS^T as B
+//   operand straight from the accumulator).
 // * Keys outside a row's range get S = -inf, so P = 0 exactly; a row with no
 //   legal key (or a padding row) carries LSE = Delta = 0 and bounds [0, 0),
 //   is masked everywhere and contributes nothing.
@@ -89,7 +92,7 @@ struct BwdParams {
   uint16_t* qp;              // [blocks][32 rows][128]
   uint16_t* dop;
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
-  int32_t seq_q, seq_kv, total_kv, kv_tiles, kv_tiles_dkv;
+  int32_t seq_q, seq_kv, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
   float scale;               // sm_scale
@@ -682,7 +685,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // Host side.
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int64_t blocks[2], items[2], total_blocks, kv_tiles, kv_tiles_dkv;
+  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv;
   size_t off_info, off_qp, off_dop, off_ranges, bytes;
 };
 
@@ -697,7 +700,6 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
     L.items[b] = ceil_div(n[b] * group, kRowsPerItem);
   }
   L.total_blocks = static_cast<int64_t>(heads_kv) * (L.blocks[0] + L.blocks[1]);
-  L.kv_tiles = ceil_div(total_kv, kBN);
   L.kv_tiles_dkv = ceil_div(total_kv, kKeysDkv);
   size_t o = 0;
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
@@ -802,7 +804,6 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.seq_q = static_cast<int32_t>(seq_q);
   p.seq_kv = static_cast<int32_t>(seq_kv);
   p.total_kv = static_cast<int32_t>(total_kv);
-  p.kv_tiles = static_cast<int32_t>(L.kv_tiles);
   p.kv_tiles_dkv = static_cast<int32_t>(L.kv_tiles_dkv);
   p.hq = heads_q;
   p.hkv = heads_kv;
