@@ -84,11 +84,7 @@ static_assert(kRowsPerLoader % 4 == 0, "a wave stages whole 1 KiB blocks of K an
 constexpr int kLoads = kRowsPerLoader / 4;            // loads per lane per K (or V^T) tile
 static_assert(kLoads == 1 || kLoads == 2 || kLoads == 4, "loads spread over 8 / 4 k-steps");
 constexpr float kMaxSentinel = -1073741824.0f;        // -2^30 (V:174)
-// Epilogue staging of O in the (then idle) LDS rings: 32 rows per wave at a
-// 272-byte stride (16 bytes of padding spread the rows over the banks),
-// followed by each row's global offset.
-constexpr int kORowBytes = kRowBytes + 16;
-static_assert(kWaves * kRowsPerWave * (kORowBytes + 8) <= kLdsBytes, "O staging fits the rings");
+static_assert(kWaves * kStoreRegionBytes <= kLdsBytes, "the O epilogue fits the rings");
 
 struct FwdParams {
   const uint16_t* q;
@@ -532,38 +528,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   }
 
   // ---- epilogue: normalise, write O rows and log2-LSE -------------------------
-  // O goes through LDS so that each store instruction writes four whole
-  // 256-byte rows (direct stores from the O^T accumulator layout would write
-  // 16 bytes into each of 32 rows).  The rings are free once every wave's
-  // last loads (empty descriptors) have landed and every wave is past its
-  // last tile.
+  // O goes out as whole rows through LDS (store_rows_via_lds).  The rings are
+  // free once every wave's last loads (empty descriptors) have landed and
+  // every wave is past its last tile.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  char* ob = smem + wave * kRowsPerWave * kORowBytes;
-  int64_t* rowoff = reinterpret_cast<int64_t*>(smem + kWaves * kRowsPerWave * kORowBytes) +
-                    wave * kRowsPerWave;
-  {
-    const float inv = 1.0f / w.l;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint2 u;
-        u.x = pack_bf16x2(w.o[d][4 * j + 0] * inv, w.o[d][4 * j + 1] * inv);
-        u.y = pack_bf16x2(w.o[d][4 * j + 2] * inv, w.o[d][4 * j + 3] * inv);
-        *reinterpret_cast<uint2*>(ob + rl * kORowBytes + 2 * (32 * d + 8 * j + 4 * hh)) = u;
-      }
-    }
-    if (hh == 0) rowoff[rl] = valid ? (static_cast<int64_t>(pos) * p.hq + qh) * kD : -1;
-    if (valid && hh == 0) p.lse[static_cast<int64_t>(pos) * p.hq + qh] = log2f(w.l) + w.m * w.c;
-  }
-  // The wave reads back only what it wrote: its LDS operations complete in order.
-#pragma unroll
-  for (int i = 0; i < kRowsPerWave / 4; ++i) {
-    const int row = 4 * i + (lane >> 4), c = lane & 15;
-    const int64_t off = rowoff[row];
-    const uint4 v = *reinterpret_cast<const uint4*>(ob + row * kORowBytes + 16 * c);
-    if (off >= 0) *reinterpret_cast<uint4*>(p.out + off + 8 * c) = v;
-  }
+  if (valid && hh == 0) p.lse[static_cast<int64_t>(pos) * p.hq + qh] = log2f(w.l) + w.m * w.c;
+  store_rows_via_lds(smem + wave * kStoreRegionBytes,
+                     valid ? (static_cast<int64_t>(pos) * p.hq + qh) * kD : -1, w.o, 1.0f / w.l,
+                     p.out, lane);
 }
 
 }  // namespace

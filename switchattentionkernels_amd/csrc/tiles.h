@@ -135,6 +135,42 @@ __global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict
 }
 }  // namespace
 
+// Row store through LDS.  A wave holds a 32 x 128 tile in the MFMA
+// accumulator layout (acc[d][4j + i] of lane (r = lane % 32, h = lane / 32)
+// is row r, column 32d + 8j + 4h + i); written to memory directly, each
+// store instruction would put 16 bytes into each of 32 rows.  Staged through
+// the wave's LDS region (32 rows at a 272-byte stride, then 32 row offsets),
+// each store instruction writes four whole 256-byte rows.  row_off is the
+// element offset of this lane's row in out, or -1 to skip the row.  The wave
+// reads back only what it wrote (its LDS operations complete in order); the
+// caller makes sure nothing else uses the region meanwhile.
+constexpr int kORowBytes = kRowBytes + 16;
+constexpr int kStoreRegionBytes = 32 * kORowBytes + 32 * 8;
+__device__ __forceinline__ void store_rows_via_lds(char* region, int64_t row_off,
+                                                   const f32x16 (&acc)[4], float scale,
+                                                   uint16_t* __restrict__ out, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+  int64_t* offs = reinterpret_cast<int64_t*>(region + 32 * kORowBytes);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint2 u;
+      u.x = pack_bf16x2(acc[d][4 * j + 0] * scale, acc[d][4 * j + 1] * scale);
+      u.y = pack_bf16x2(acc[d][4 * j + 2] * scale, acc[d][4 * j + 3] * scale);
+      *reinterpret_cast<uint2*>(region + r * kORowBytes + 2 * (32 * d + 8 * j + 4 * h)) = u;
+    }
+  }
+  if (h == 0) offs[r] = row_off;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = 4 * i + (lane >> 4), c = lane & 15;
+    const int64_t off = offs[row];
+    const uint4 v = *reinterpret_cast<const uint4*>(region + row * kORowBytes + 16 * c);
+    if (off >= 0) *reinterpret_cast<uint4*>(out + off + 8 * c) = v;
+  }
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace tiles
