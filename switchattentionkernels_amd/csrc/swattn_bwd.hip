@@ -742,6 +742,10 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
     return invalid("swattn_prefill_bwd: bad shape");
   if (heads_q % heads_kv != 0)
     return invalid("swattn_prefill_bwd: heads_q must be a multiple of heads_kv");
+  // Per-lane staging offsets inside a key tile are 32-bit: (rows of a tile) x
+  // heads_kv x 256 bytes must stay below 2^31.
+  if (heads_kv > 4096 || heads_q > 65536)
+    return invalid("swattn_prefill_bwd: at most 4096 KV heads and 65536 query heads");
   if (window <= 0) return invalid("swattn_prefill_bwd: window must be positive");
   if (!(scale_log2 > 0.f) || !isfinite(scale_log2))
     return invalid("swattn_prefill_bwd: scale_log2 must be positive and finite");
@@ -757,10 +761,12 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   const bool meta = full_starts != nullptr || local_starts != nullptr || causal_ends != nullptr;
   if (meta && (full_starts == nullptr || local_starts == nullptr || causal_ends == nullptr))
     return invalid("swattn_prefill_bwd: metadata needs full_starts, local_starts and causal_ends");
-  if (q == nullptr || k == nullptr || v == nullptr || dk == nullptr || dv == nullptr)
+  // dk / dv are written for every key even without query rows (as zeros);
+  // the row-side buffers are only needed when there are rows.
+  if (k == nullptr || v == nullptr || dk == nullptr || dv == nullptr)
     return invalid("swattn_prefill_bwd: null pointer");
   if (n_full + n_local > 0 &&
-      (out == nullptr || lse == nullptr || dout == nullptr || dq == nullptr ||
+      (q == nullptr || out == nullptr || lse == nullptr || dout == nullptr || dq == nullptr ||
        (n_full > 0 && full_idx == nullptr) || (n_local > 0 && local_idx == nullptr)))
     return invalid("swattn_prefill_bwd: null pointer");
   const BwdLayout L = bwd_layout(total_kv, heads_kv, group, n_full, n_local);

@@ -567,6 +567,10 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
     return invalid("swattn_prefill_fwd: bad shape");
   if (heads_q % heads_kv != 0)
     return invalid("swattn_prefill_fwd: heads_q must be a multiple of heads_kv");
+  // Per-lane staging offsets inside a key tile are 32-bit: (rows of a tile) x
+  // heads_kv x 256 bytes must stay below 2^31.
+  if (heads_kv > 4096 || heads_q > 65536)
+    return invalid("swattn_prefill_fwd: at most 4096 KV heads and 65536 query heads");
   if (window <= 0) return invalid("swattn_prefill_fwd: window must be positive");
   if (n_full < 0 || n_local < 0 || n_full + n_local > static_cast<int64_t>(batch) * seq_q)
     return invalid("swattn_prefill_fwd: bad index counts");

@@ -225,3 +225,17 @@ def test_s16k_backward_identities_and_sampled_rows():
                                      [0, 1, 1023, 1024, s - 1]]))
     rq, _, _ = _oracle(q, k, v, do, m, w, rows=rows)
     _grad_close(dq, rq, "s16k dq sampled rows", rows=torch.as_tensor(rows))
+
+
+def test_backward_with_no_query_rows():
+    """No query rows: dq is empty and every key gets dk = dv = 0."""
+    q = torch.zeros(1, 0, 4, 128, dtype=torch.bfloat16, device=DEV)
+    k = torch.randn(1, 70, 2, 128, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, 70, 2, 128, device=DEV).to(torch.bfloat16)
+    full, local = build_switch_query_indices(torch.zeros(1, 0, dtype=torch.bool, device=DEV))
+    o, lse = switch_gqa_prefill_forward(q, k, v, full, local, window_size=8)
+    dq, dk, dv = switch_gqa_prefill_backward(q, k, v, o, lse, torch.zeros_like(q), full, local,
+                                             window_size=8)
+    torch.cuda.synchronize()
+    assert dq.shape == q.shape
+    assert torch.count_nonzero(dk) == 0 and torch.count_nonzero(dv) == 0
