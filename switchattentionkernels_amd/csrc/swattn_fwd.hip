@@ -84,7 +84,9 @@ static_assert(kRowsPerLoader % 4 == 0, "a wave stages whole 1 KiB blocks of K an
 constexpr int kLoads = kRowsPerLoader / 4;            // loads per lane per K (or V^T) tile
 static_assert(kLoads == 1 || kLoads == 2 || kLoads == 4, "loads spread over 8 / 4 k-steps");
 constexpr float kMaxSentinel = -1073741824.0f;        // -2^30 (V:174)
-static_assert(kWaves * kStoreRegionBytes <= kLdsBytes, "the O epilogue fits the rings");
+// The rings, or the O epilogue's staging if that is larger (eight waves).
+constexpr int kSmemBytes = kLdsBytes > kWaves * kStoreRegionBytes ? kLdsBytes
+                                                                   : kWaves * kStoreRegionBytes;
 
 struct FwdParams {
   const uint16_t* q;
@@ -419,7 +421,7 @@ __device__ __forceinline__ void pipe_step(const FwdParams& p, const StagePlan& s
 template <bool kMeta>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void fwd_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kSmemBytes];
   __shared__ int s_range[2 * kWaves];
 
   const int tid = threadIdx.x;
