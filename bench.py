@@ -84,7 +84,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                          "(sharding across GPUs is described in DESIGN.md, not implemented)"}))
+                          "(sharding across GPUs is designed, not implemented)"}))
         sys.exit(2)
 
     from switchattentionkernels_amd import (build_switch_query_indices, routed_flops,
