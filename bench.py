@@ -60,6 +60,9 @@ def parse():
                     help="only loop the attention kernel (for rocprofv3 runs)")
     ap.add_argument("--backward-only", action="store_true",
                     help="only loop switch_gqa_prefill_backward (for rocprofv3 runs)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only loop switch_gqa_decode_forward on the decode comparator's "
+                         "workload (for rocprofv3 runs)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="with --kernel-only: also run 3 device copies of this many MiB "
                          "(calibrates the HBM byte counters)")
@@ -78,6 +81,29 @@ def time_launches(fn, iters, warmup=3):
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / iters
+
+
+def decode_comparator(args, dev, HQ, HKV, D, W, iters, warmup):
+    """Routed decode on 64 sequences with 8192-key caches, Bernoulli(p_full)
+    routing: time per call and the HBM rate of its algorithmic bytes (the
+    routed K and V rows, plus Q and O)."""
+    from switchattentionkernels_amd import switch_gqa_decode_forward
+    db, dl = 64, 8192
+    gen = torch.Generator().manual_seed(args.seed)
+    dq = torch.randn(db, 1, HQ, D, generator=gen).to(torch.bfloat16).to(dev)
+    dk = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+    dv = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+    dlens = torch.full((db,), dl, dtype=torch.int32, device=dev)
+    dfull = (torch.rand(db, generator=gen) < args.p_full).to(dev)
+    dkeys = sum(dl if f else min(dl, W) for f in dfull.tolist())
+    dbytes = dkeys * HKV * D * 2 * 2 + 2 * db * HQ * D * 2
+    dec_ms = time_launches(lambda: switch_gqa_decode_forward(dq, dk, dv, dlens, dfull,
+                                                              window_size=W), iters, warmup=warmup)
+    return {"workload": f"B{db} cache {dl} Hq{HQ}/Hkv{HKV} W{W} p_full={args.p_full}, "
+                        f"{int(dfull.sum())} full",
+            "us": round(dec_ms * 1e3, 1), "hbm_gbs": round(dbytes / (dec_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(dbytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3),
+            "bytes": dbytes}
 
 
 def main():
@@ -143,6 +169,12 @@ def main():
         print(json.dumps({"kernel_only": True, "launches": args.warmup + args.steps,
                           "timed_launches": args.steps, "entry_point_ms": round(kernel_ms, 4),
                           "calibration": calib}))
+        return
+
+    if args.decode_only:
+        res = decode_comparator(args, dev, HQ, HKV, D, W, args.steps, args.warmup)
+        print(json.dumps({"decode_only": True, "launches": args.warmup + args.steps,
+                          "timed_launches": args.steps, **res}))
         return
 
     if args.backward_only:
@@ -226,22 +258,7 @@ def main():
     # ---- routed decode (extension): one token per sequence over its KV cache ------
     decode = None
     try:
-        from switchattentionkernels_amd import switch_gqa_decode_forward
-        db, dl = 64, 8192
-        gen = torch.Generator().manual_seed(args.seed)
-        dq = torch.randn(db, 1, HQ, D, generator=gen).to(torch.bfloat16).to(dev)
-        dk = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
-        dv = torch.randn(db, dl, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
-        dlens = torch.full((db,), dl, dtype=torch.int32, device=dev)
-        dfull = (torch.rand(db, generator=gen) < args.p_full).to(dev)
-        dkeys = sum(dl if f else min(dl, W) for f in dfull.tolist())
-        dbytes = dkeys * HKV * D * 2 * 2 + 2 * db * HQ * D * 2
-        dec_ms = time_launches(lambda: switch_gqa_decode_forward(dq, dk, dv, dlens, dfull,
-                                                                  window_size=W), 20, warmup=5)
-        decode = {"workload": f"B{db} cache {dl} Hq{HQ}/Hkv{HKV} W{W} p_full={args.p_full}",
-                  "us": round(dec_ms * 1e3, 1), "hbm_gbs": round(dbytes / (dec_ms * 1e-3) / 1e9, 1),
-                  "hbm_frac": round(dbytes / (dec_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 3)}
-        del dq, dk, dv
+        decode = decode_comparator(args, dev, HQ, HKV, D, W, 20, 5)
     except Exception as exc:  # comparator only
         print(f"[bench] decode comparator unavailable: {exc}", file=sys.stderr, flush=True)
 
