@@ -313,7 +313,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   // [V tile: 256 key rows][three block slots]
   __shared__ __attribute__((aligned(1024))) char smem[kVTileBytes + kRingSlots * kStageBytes];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // The wave index as a scalar: per-wave choices (which block part a wave
+  // stages, its source pointer) then stay scalar selects.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, h = lane >> 5;
   const int t = blockIdx.x / p.hkv, kvh = blockIdx.x - (blockIdx.x / p.hkv) * p.hkv;
   const int kw0 = t * kKeysDkv + 32 * wave;   // this wave's first key
@@ -329,6 +331,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) kf[kk] = bf16x8{};
   }
+  // Wait for the K loads with the builtin, before any LDS load is issued:
+  // the compiler then knows they are complete.  Otherwise it keeps them
+  // outstanding into the block loop and waits for them at their first use
+  // there with vmcnt counts that also drain the next blocks' LDS loads.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   f32x16 dkt[4], dvt[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) dkt[d] = dvt[d] = f32x16{};
@@ -512,7 +519,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   __shared__ __attribute__((aligned(1024))) char smem[kRingSlots * kQStageBytes];
   __shared__ int s_range[2 * kBwdWaves];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // The wave index as a scalar: per-wave choices (which block part a wave
+  // stages, its source pointer) then stay scalar selects.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, h = lane >> 5;
   const int kvh = blockIdx.x % p.hkv;
   const int t = blockIdx.x / p.hkv;
@@ -546,6 +555,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qf[kk] = dof[kk] = bf16x8{};
   }
+  // As in the dK/dV kernel: the row loads complete here, known to the
+  // compiler, so that no wait in the tile loop drains the tile LDS loads.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   const bool has = valid && ks < ke;
   const int w_min_s = wave_min(has ? ks : INT_MAX);
   const int w_max_e = wave_max(has ? ke : INT_MIN);
