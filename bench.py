@@ -218,6 +218,19 @@ def main():
                                                         cnt.data_ptr(), ws.data_ptr(), ws_bytes,
                                                         stream), 50)
     compact_bytes = S * B + 4 * S * B + 8
+    # The fused router step (extension): bf16 logits > 0 compacted in one pass.
+    logits = torch.randn(S * B, generator=torch.Generator().manual_seed(args.seed + 2))
+    logits = logits.to(torch.bfloat16).to(dev)
+    logits_ms = time_launches(lambda: L.swattn_compact_logits(
+        logits.data_ptr(), 1, S * B, 0.0, idx.data_ptr(), cnt.data_ptr(), ws.data_ptr(),
+        ws_bytes, stream), 50)
+    # The split-key merge (extension): two partial (O, LSE) pairs of this
+    # prefill's shape folded into one; HBM bytes = 2 partials in, 1 out.
+    from switchattentionkernels_amd import merge_attention_partials
+    lse_b = lse.clone()
+    merge_ms = time_launches(lambda: merge_attention_partials([out, out], [lse, lse_b]), 20)
+    merge_bytes = 3 * (out.numel() * 2 + lse.numel() * 4)
+    del lse_b
     print(f"[bench] attention kernel {attn_ms:.3f} ms ({attn_tflops:.1f} TFLOP/s); dense causal "
           f"{dense_ms:.3f} ms; compaction {compact_ms * 1e3:.1f} us", file=sys.stderr, flush=True)
 
@@ -365,6 +378,9 @@ def main():
             "sdpa_flash_causal_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
             "compaction_us": round(compact_ms * 1e3, 2),
             "compaction_gbs": round(compact_bytes / (compact_ms * 1e-3) / 1e9, 1),
+            "compaction_logits_us": round(logits_ms * 1e3, 2),
+            "merge_two_partials_us": round(merge_ms * 1e3, 1),
+            "merge_hbm_gbs": round(merge_bytes / (merge_ms * 1e-3) / 1e9, 1),
             "decode": decode,
             "backward": backward,
         },
