@@ -78,3 +78,39 @@ def test_tensors_past_2gib_sampled_rows():
     mx = float(e.abs().max() / rq[0].abs().max())
     print(f"[large] dq sampled rows: rel_l2 {l2:.2e} rel_max {mx:.2e}", flush=True)
     assert l2 <= 1e-2 and mx <= 3e-2
+
+
+def test_decode_caches_past_2gib():
+    """Decode over [16, 131072, 8, 128] caches (4 GiB each, 2^31 elements):
+    the last sequences' keys sit past byte offset 3 GiB.  The oracle runs per
+    sequence on the routed slice of its cache ([lo, n) as a whole cache of
+    n - lo keys, routed full), which is the same problem."""
+    from switchattentionkernels_amd import switch_gqa_decode_forward
+    b, L, hq, hkv, w = 16, 131072, 32, 8, 4096
+    g = torch.Generator(device=DEV).manual_seed(22)
+    q = torch.randn(b, hq, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(b, L, hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(b, L, hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    assert k.numel() * k.element_size() >= 2 ** 32
+    lens = [1, 5000, 9000, 70000, 30, L, 100, 64, 4097, 4096, 20000, 77777, 3, L - 1, 100000, L]
+    full = [True, False, False, True, False, True, True, False,
+            False, True, False, True, False, False, True, True]
+    print(f"[large] decode B{b} L{L} Hq{hq}/Hkv{hkv} W{w}", flush=True)
+    o, lse = switch_gqa_decode_forward(q, k, v, torch.tensor(lens, dtype=torch.int32, device=DEV),
+                                       torch.tensor(full, device=DEV), window_size=w)
+    torch.cuda.synchronize()
+    o, lse = o.float().cpu(), lse.cpu()
+    worst = 0.0
+    for i in range(b):
+        n = lens[i]
+        lo = 0 if full[i] else max(n - w, 0)
+        o_r, lse_r = oracle.decode_attention(q[i:i + 1].cpu(), k[i:i + 1, lo:n].cpu(),
+                                             v[i:i + 1, lo:n].cpu(), [n - lo], [True],
+                                             window_size=w)
+        err = (o[i] - o_r[0]).abs()
+        lerr = ((lse[i] - lse_r[0]).abs() / lse_r[0].abs().clamp(min=1.0)).max().item()
+        assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3 and lerr <= 1e-3, (
+            f"sequence {i}: O max {err.max().item():.3e} mean {err.mean().item():.3e} "
+            f"LSE rel {lerr:.3e}")
+        worst = max(worst, err.max().item())
+    print(f"[large] decode: worst O max-abs {worst:.3e}", flush=True)
