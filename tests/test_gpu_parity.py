@@ -459,6 +459,28 @@ def test_c_abi_writes_only_listed_rows():
     assert torch.equal(out[0][m], ref_o[0][m]) and torch.equal(lse[0][m], ref_l[0][m])
 
 
+def test_every_row_written_s16k_canary():
+    """Config #3 through the C ABI into O / LSE pre-filled with NaN: every
+    row sees at least one key, so any NaN left behind is a row the kernel
+    never wrote (a scatter gap or a lost race)."""
+    wl = workloads.build("s16k", seed=6, p_full=0.25)
+    q, k, v = (wl[x].to(DEV) for x in ("q", "k", "v"))
+    full, local = build_switch_query_indices(wl["mask"].to(DEV))
+    out = torch.full_like(q, float("nan"))
+    lse = torch.full(q.shape[:3], float("nan"), device=DEV)
+    L = _lib.lib()
+    ws_bytes = L.swattn_prefill_workspace_bytes(1, 16384, 8, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(),
+                              full.numel(), local.data_ptr(), local.numel(), None, None, None,
+                              out.data_ptr(), lse.data_ptr(), 1, 16384, 16384, 32, 8, 128,
+                              wl["window"], ctypes.c_float(128 ** -0.5 * oracle.LOG2E),
+                              ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any().item() and not torch.isnan(lse).any().item()
+
+
 # ----------------------------------------------------------------------------
 # committed golden fixtures
 # ----------------------------------------------------------------------------
