@@ -13,46 +13,13 @@ import threading
 
 import torch  # noqa: F401  -- loads PyTorch's HIP runtime before the library
 
+from ._abi import SIGNATURES, bind  # noqa: F401  -- SIGNATURES is part of this module's API
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libswattn.so")
 
 _lock = threading.Lock()
 _lib = None
-
-_i32p = ctypes.POINTER(ctypes.c_int32)
-_vp = ctypes.c_void_p
-_i64 = ctypes.c_int64
-_i32 = ctypes.c_int32
-
-# name -> (restype, argtypes); must mirror include/swattn.h exactly.
-SIGNATURES = {
-    "swattn_version": (ctypes.c_int, []),
-    "swattn_last_error": (ctypes.c_char_p, []),
-    "swattn_compact_workspace_bytes": (ctypes.c_size_t, [_i64]),
-    "swattn_compact": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp]),
-    "swattn_compact_logits": (ctypes.c_int, [_vp, _i32, _i64, ctypes.c_float, _vp, _vp, _vp,
-                                             ctypes.c_size_t, _vp]),
-    "swattn_check_indices": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
-    "swattn_build_metadata": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _i32,
-                                             _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "swattn_prefill_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32]),
-    "swattn_decode_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32]),
-    "swattn_decode_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32,
-                                         _i32, _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t,
-                                         _vp]),
-    "swattn_shard_bounds": (ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
-    "swattn_merge_partials": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i32, _vp,
-                                             _vp, _i64, _i32, _vp]),
-    "swattn_prefill_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
-                                          _vp, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
-                                          ctypes.c_float, _vp, ctypes.c_size_t, _vp]),
-    "swattn_prefill_bwd_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32, _i32, _i64,
-                                                             _i64]),
-    "swattn_prefill_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
-                                          _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32,
-                                          _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t, _vp]),
-    "swattn_mfma_peak": (ctypes.c_int, [_i64, _i32, _vp, _vp]),
-}
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -70,12 +37,7 @@ def lib() -> ctypes.CDLL:
                 raise LibraryNotBuilt(
                     f"{LIB_PATH} is missing: build it with "
                     "`python -m switchattentionkernels_amd.build`")
-            h = ctypes.CDLL(LIB_PATH)
-            for name, (res, args) in SIGNATURES.items():
-                fn = getattr(h, name)
-                fn.restype = res
-                fn.argtypes = args
-            _lib = h
+            _lib = bind(ctypes.CDLL(LIB_PATH))
     return _lib
 
 

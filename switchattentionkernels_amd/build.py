@@ -63,14 +63,15 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile ``libswattn.so``; returns its path.  Always recompiles."""
-    cmd = [_hipcc()] + compile_flags()
+def build(verbose: bool = False, out: str = LIB, extra_flags=()) -> str:
+    """Compile ``libswattn.so`` (or ``out``, with ``extra_flags`` appended to
+    the compile flags); returns its path.  Always recompiles."""
+    cmd = [_hipcc()] + compile_flags() + list(extra_flags)
     tl = _torch_lib_dir()
     if tl is not None:
         cmd += ["-L", tl, "-Wl,-rpath," + tl]
     cmd += [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     cmd += ["-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -81,8 +82,8 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
     if verbose and err:
         print(err, file=sys.stderr)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
