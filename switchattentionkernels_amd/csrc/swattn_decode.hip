@@ -79,9 +79,12 @@ __device__ __forceinline__ void key_range(const DecodeParams& p, int b, int64_t&
 // chunks per KV head.  Work items are numbered sequence by sequence, KV head
 // by KV head, chunk by chunk.
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanLdsSeqs = 4096;   // sequences whose first item and chunk count stay in LDS
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeParams p) {
   __shared__ int64_t s_red[kPlanThreads / 64];
   __shared__ int64_t s_scan[kPlanThreads];
+  __shared__ int32_t s_first[kPlanLdsSeqs], s_n[kPlanLdsSeqs];
+  const bool in_lds = p.batch <= kPlanLdsSeqs;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (p.batch + kPlanThreads - 1) / kPlanThreads;
   const int b0 = min(tid * per, p.batch), b1 = min(b0 + per, p.batch);
@@ -126,6 +129,10 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
     const int64_t n = (hi - lo + chunk - 1) / chunk;
     p.plan[2 + 2 * b] = run * p.hkv;
     p.plan[3 + 2 * b] = n;
+    if (in_lds) {
+      s_first[b] = static_cast<int32_t>(run * p.hkv);
+      s_n[b] = static_cast<int32_t>(n);
+    }
     run += n;
   }
   const int64_t items = s_scan[kPlanThreads - 1] * p.hkv;
@@ -136,14 +143,23 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(const DecodeP
   __syncthreads();   // every sequence's first item and chunk count are written
   // Work items, one per thread at a time: item i belongs to the last
   // sequence whose first item is <= i (sequences without keys own none).
+  // The search runs in LDS when the sequences fit there (item counts stay
+  // below 2^31: at most target + pairs).
   for (int64_t i = tid; i < items; i += kPlanThreads) {
     int lo = 0, hi = p.batch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (p.plan[2 + 2 * mid] <= i) lo = mid; else hi = mid - 1;
+    if (in_lds) {
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_first[mid] <= i) lo = mid; else hi = mid - 1;
+      }
+    } else {
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (p.plan[2 + 2 * mid] <= i) lo = mid; else hi = mid - 1;
+      }
     }
-    const int64_t r = i - p.plan[2 + 2 * lo];
-    const int64_t n = p.plan[3 + 2 * lo];
+    const int64_t r = i - (in_lds ? s_first[lo] : p.plan[2 + 2 * lo]);
+    const int64_t n = in_lds ? s_n[lo] : p.plan[3 + 2 * lo];
     const int kvh = static_cast<int>(r / n);
     p.items[i] = make_int2(lo * p.hkv + kvh, static_cast<int>(r - static_cast<int64_t>(kvh) * n));
   }

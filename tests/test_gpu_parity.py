@@ -628,6 +628,23 @@ def test_decode_plan_with_long_mixed_caches():
                   tag="decode long mixed")
 
 
+def test_decode_plan_beyond_lds_sequence_table():
+    """More sequences (5000) than the plan kernel keeps in LDS (4096): the
+    work-item search then runs over the plan in global memory."""
+    gen = torch.Generator().manual_seed(78)
+    b, cache_len, hq, hkv, w = 5000, 96, 8, 2, 40
+    q = torch.randn(b, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, cache_len, hkv, 128, generator=gen).to(torch.bfloat16)
+    lens = torch.randint(0, cache_len + 1, (b,), generator=gen)
+    full = torch.rand(b, generator=gen) < 0.5
+    o, lse = switch_gqa_decode_forward(q.to(DEV), k.to(DEV), v.to(DEV),
+                                       lens.to(torch.int32).to(DEV), full.to(DEV), window_size=w)
+    o_r, lse_r = oracle.decode_attention(q, k, v, lens.tolist(), full.tolist(), window_size=w)
+    _assert_close(o.unsqueeze(1), lse.unsqueeze(1), o_r.unsqueeze(1), lse_r.unsqueeze(1),
+                  tag="decode 5000 sequences")
+
+
 def test_decode_clamps_lengths_and_matches_prefill_last_row():
     gen = torch.Generator().manual_seed(31)
     hq, hkv, cache_len, w = 16, 4, 700, 100
