@@ -352,8 +352,12 @@ __device__ __forceinline__ void pipe_body(const char* smem, const StagePlan& sp,
   f32x16& c1 = sb[kPar][1];
   f32x16& n0 = sb[kPar ^ 1][0];
   f32x16& n1 = sb[kPar ^ 1][1];
-  // phase A
+  // phase A.  In a full step the wave issues at raised priority during phase
+  // A (the exponentials) and at normal priority during phase B: where the two
+  // waves of a SIMD compete, phase A goes first (0.4-0.9 % faster at p_full
+  // 0.25-1 than no priorities, bit-identical).
   bf16x8 pk[4];
+  if constexpr (kS && kPV) __builtin_amdgcn_s_setprio(1);
   if constexpr (kS) {
     qk_tile(kb, w, n0, n1, sp, krs, kslot);
   } else {
@@ -384,6 +388,7 @@ __device__ __forceinline__ void pipe_body(const char* smem, const StagePlan& sp,
     }
   }
   // phase B
+  if constexpr (kS && kPV) __builtin_amdgcn_s_setprio(0);
   if constexpr (kPV) {
     pv_tile(vb, w, pk, sp, vrs, vslot);
     w.l = w.l * w.alpha + tile_sum(c0, c1);
