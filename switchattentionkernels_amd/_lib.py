@@ -7,6 +7,7 @@ never silently compute on a different path.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -52,6 +53,27 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_no_switch = contextlib.nullcontext()
+
+
+def _index(device) -> int:
+    idx = device.index
+    return torch.cuda.current_device() if idx is None else idx
+
+
 def stream_handle(device) -> int:
     """hipStream_t of torch's current stream on ``device``."""
+    if _raw_stream is not None:
+        return _raw_stream(_index(device))
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def on_device(device):
+    """``torch.cuda.device(device)``, or a context that does nothing when
+    ``device`` is already the current device (the common case, and a
+    tenth of the cost)."""
+    idx = device.index
+    if idx is None or idx == torch.cuda.current_device():
+        return _no_switch
+    return torch.cuda.device(idx)

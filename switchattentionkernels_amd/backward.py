@@ -98,7 +98,7 @@ def switch_gqa_prefill_backward(
     ws_bytes = int(L.swattn_prefill_bwd_workspace_bytes(batch, kv_len, heads, kv_heads, dim,
                                                         full.numel(), local.numel()))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         st = L.swattn_prefill_bwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), output.data_ptr(), lse.data_ptr(),
             grad_output.data_ptr(), full.data_ptr(), full.numel(), local.data_ptr(),

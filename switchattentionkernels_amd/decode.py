@@ -71,7 +71,7 @@ def switch_gqa_decode_forward(q: torch.Tensor, k_cache: torch.Tensor, v_cache: t
     L = _lib.lib()
     ws_bytes = int(L.swattn_decode_workspace_bytes(batch, cache_len, heads, kv_heads))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = L.swattn_decode_fwd(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                                  lens.data_ptr(), full.data_ptr(), out.data_ptr(), lse.data_ptr(),
                                  batch, cache_len, heads, kv_heads, dim, int(window_size), scale,

@@ -84,7 +84,7 @@ def build_switch_attention_metadata(q_len: int, kv_len: int, *, device, window_s
 
     md = SwitchAttentionMetadata(e(q_len), e(kv_len), e(q_len), e(kv_len), e(q_len), e(q_len),
                                  e(q_len))
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = _lib.lib().swattn_build_metadata(
             cq_t.data_ptr(), ck_t.data_ptr(), len(cq) - 1, q_len, kv_len, window_size,
             md.q_positions.data_ptr(), md.kv_positions.data_ptr(), md.q_segment_ids.data_ptr(),

@@ -86,7 +86,7 @@ def _prepare_indices(indices: torch.Tensor, *, device: torch.device) -> torch.Te
 def _device_flags(full: torch.Tensor, local: torch.Tensor, seq_len: int) -> int:
     """Run ``swattn_check_indices``; one 4-byte device-to-host read."""
     flags = torch.empty(1, dtype=torch.int32, device=full.device)
-    with torch.cuda.device(full.device):
+    with _lib.on_device(full.device):
         st = _lib.lib().swattn_check_indices(full.data_ptr(), full.numel(), local.data_ptr(),
                                              local.numel(), seq_len, flags.data_ptr(),
                                              _lib.stream_handle(full.device))
@@ -200,7 +200,7 @@ def build_switch_query_indices(full_mask: torch.Tensor) -> Tuple[torch.Tensor, t
     L = _lib.lib()
     ws_bytes = int(L.swattn_compact_workspace_bytes(n))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = L.swattn_compact(mask.data_ptr(), n, out.data_ptr(), counts.data_ptr(),
                               ws.data_ptr(), ws_bytes, _lib.stream_handle(dev))
     _lib.check(st, "swattn_compact")
@@ -244,7 +244,7 @@ def build_switch_query_indices_from_logits(
     L = _lib.lib()
     ws_bytes = int(L.swattn_compact_workspace_bytes(n))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = L.swattn_compact_logits(logits.data_ptr(), _LOGIT_DTYPES[logits.dtype], n, thr,
                                      out.data_ptr(), counts.data_ptr(), ws.data_ptr(), ws_bytes,
                                      _lib.stream_handle(dev))
@@ -308,7 +308,7 @@ def switch_gqa_prefill_forward(
     L = _lib.lib()
     ws_bytes = int(L.swattn_prefill_workspace_bytes(batch, kv_len, kv_heads, dim))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    with _lib.on_device(q.device):
         st = L.swattn_prefill_fwd(
             q.data_ptr(), k.data_ptr(), v.data_ptr(),
             full.data_ptr(), full.numel(), local.data_ptr(), local.numel(),

@@ -49,7 +49,7 @@ def shard_attention_metadata(q_positions: torch.Tensor, *, kv_start: int, kv_end
     full_starts = torch.empty(n, dtype=torch.int32, device=dev)
     local_starts = torch.empty_like(full_starts)
     causal_ends = torch.empty_like(full_starts)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = _lib.lib().swattn_shard_bounds(pos.data_ptr(), n, int(kv_start), int(kv_end),
                                             int(window_size), full_starts.data_ptr(),
                                             local_starts.data_ptr(), causal_ends.data_ptr(),
@@ -92,7 +92,7 @@ def merge_attention_partials(outputs: Sequence[torch.Tensor],
     o_ptrs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     l_ptrs = (ctypes.c_void_p * n)(*[l.data_ptr() for l in ls])
     dev = out.device
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         st = _lib.lib().swattn_merge_partials(o_ptrs, l_ptrs, n, out.data_ptr(), lse.data_ptr(),
                                               lse.numel(), 128, _lib.stream_handle(dev))
     _lib.check(st, "swattn_merge_partials")
