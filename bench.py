@@ -26,6 +26,9 @@ The JSON line also carries:
   SDPA causal (flash backend) on the same shape, the compaction alone, the
   routed decode extension (64 sequences, 8192-key caches) against HBM, and
   the routed backward (dq, dk, dv) of the same prefill.
+
+``--configs cpu,b2,s16k,varlen,s64k`` instead times the forward and the
+backward on each named workload (one JSON line each, no roofline).
 """
 
 from __future__ import annotations
@@ -63,6 +66,10 @@ def parse():
     ap.add_argument("--decode-only", action="store_true",
                     help="only loop switch_gqa_decode_forward on the decode comparator's "
                          "workload (for rocprofv3 runs)")
+    ap.add_argument("--configs", default="",
+                    help="comma-separated workloads (cpu,b2,s16k,varlen,s64k): time the "
+                         "forward and the backward on each once the clock has settled, one "
+                         "JSON line per workload")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="with --kernel-only: also run 3 device copies of this many MiB "
                          "(calibrates the HBM byte counters)")
@@ -81,6 +88,60 @@ def time_launches(fn, iters, warmup=3):
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / iters
+
+
+def settled_ms(fn, min_iters=10):
+    """Average ms per call after about 0.4 s of back-to-back calls (the
+    clock rises for tens of milliseconds from idle), over at least 0.3 s."""
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    one = max(time.perf_counter() - t0, 1e-5)
+    return time_launches(fn, max(min_iters, int(0.3 / one)), warmup=max(3, int(0.4 / one)))
+
+
+def config_table(args):
+    """Forward and backward of each named workload: routed FLOPs, time and
+    rate (backward on the 2.5 x forward-FLOP convention)."""
+    from switchattentionkernels_amd import (build_switch_attention_metadata,
+                                            build_switch_query_indices, routed_flops,
+                                            switch_gqa_prefill_backward,
+                                            switch_gqa_prefill_forward, workloads)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    for name in args.configs.split(","):
+        wl = workloads.build(name, seed=args.seed)
+        q, k, v, m = (wl[x].to(dev) for x in ("q", "k", "v", "mask"))
+        W = wl["window"]
+        full, local = build_switch_query_indices(m)
+        md = None
+        if wl["cu_seqlens"] is not None:
+            md = build_switch_attention_metadata(q.shape[1], k.shape[1], device=dev, window_size=W,
+                                                 cu_seqlens=wl["cu_seqlens"])
+        flops = routed_flops(full, local, batch=q.shape[0], seq_q=q.shape[1], seq_kv=k.shape[1],
+                             heads_q=q.shape[2], head_dim=128, window=W, metadata=md)
+
+        def fwd():
+            return switch_gqa_prefill_forward(q, k, v, full, local, window_size=W, metadata=md)
+
+        f_ms = settled_ms(fwd)
+        o, lse = fwd()
+        gen = torch.Generator().manual_seed(args.seed + 1)
+        do = torch.randn(q.shape, generator=gen).to(torch.bfloat16).to(dev)
+        b_ms = settled_ms(lambda: switch_gqa_prefill_backward(q, k, v, o, lse, do, full, local,
+                                                              window_size=W, metadata=md))
+        print(json.dumps({
+            "config": name,
+            "shape": f"B{q.shape[0]} S{q.shape[1]} Hq{q.shape[2]}/Hkv{k.shape[2]} W{W}",
+            "routed_gflop": round(flops / 1e9, 1),
+            "fwd_ms": round(f_ms, 4), "fwd_tflops": round(flops / f_ms / 1e9, 1),
+            "fwd_frac_of_peak": round(flops / f_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "bwd_ms": round(b_ms, 4), "bwd_tflops_2p5x": round(2.5 * flops / b_ms / 1e9, 1)}),
+            flush=True)
+        del q, k, v, m, o, lse, do, full, local, md
+        torch.cuda.empty_cache()
 
 
 def decode_comparator(args, dev, HQ, HKV, D, W, iters, warmup):
@@ -112,6 +173,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                           "(sharding across GPUs is designed, not implemented)"}))
         sys.exit(2)
+
+    if args.configs:
+        config_table(args)
+        return
 
     from switchattentionkernels_amd import (build_switch_query_indices, routed_flops,
                                             switch_gqa_prefill_forward, workloads)
