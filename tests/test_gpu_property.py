@@ -1,5 +1,6 @@
 """Property-based sweeps over small shapes (hypothesis): the HIP forward, the
-HIP backward and the compaction against the CPU oracle.
+HIP backward, the compaction, the routed decode and split-then-merged key
+ranges against the CPU oracle.
 
 The examples are derandomized: every run draws the same fixed set of shapes
 (batch, lengths, head counts, group size, window, routing density, key
@@ -18,10 +19,11 @@ from hypothesis import strategies as st
 
 import oracle
 from oracle import routing as R
-from switchattentionkernels_amd import (build_switch_query_indices, switch_gqa_prefill_backward,
-                                        switch_gqa_prefill_forward, workloads)
+from switchattentionkernels_amd import (build_switch_query_indices, switch_gqa_decode_forward,
+                                        switch_gqa_prefill_backward, switch_gqa_prefill_forward,
+                                        workloads)
 
-from test_gpu_parity import _assert_close
+from test_gpu_parity import _assert_close, _split_run
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -101,3 +103,69 @@ def test_compaction_property(b, s, p, seed):
     flat = mask.reshape(-1)
     assert torch.equal(full.cpu(), torch.nonzero(flat).flatten().to(torch.int32))
     assert torch.equal(local.cpu(), torch.nonzero(~flat).flatten().to(torch.int32))
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(c=st.fixed_dictionaries({
+    "b": st.integers(1, 40),
+    "cache": st.integers(1, 3000),
+    "hkv": st.integers(1, 3),
+    "g": st.sampled_from([1, 2, 3, 4, 5, 8]),
+    "w": st.integers(1, 2000),
+    "p": st.sampled_from([0.0, 0.3, 1.0]),
+    "empty": st.sampled_from([0.0, 0.2]),
+    "seed": st.integers(0, 2 ** 16),
+}))
+def test_decode_property(c):
+    """Routed decode over random cache lengths (some empty), group sizes,
+    windows and routing, against the oracle."""
+    gen = torch.Generator().manual_seed(c["seed"])
+    b, cache, hkv = c["b"], c["cache"], c["hkv"]
+    hq = c["g"] * hkv
+    q = torch.randn(b, hq, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(b, cache, hkv, 128, generator=gen).to(torch.bfloat16)
+    v = torch.randn(b, cache, hkv, 128, generator=gen).to(torch.bfloat16)
+    lens = torch.randint(0, cache + 1, (b,), generator=gen)
+    lens[torch.rand(b, generator=gen) < c["empty"]] = 0
+    full = torch.rand(b, generator=gen) < c["p"]
+    tag = f"decode b{b} cache{cache} {hq}/{hkv} w{c['w']} p{c['p']} seed{c['seed']}"
+    print(f"[property] {tag}", flush=True)
+    o, lse = switch_gqa_decode_forward(q.to(DEV), k.to(DEV), v.to(DEV),
+                                       lens.to(torch.int32).to(DEV), full.to(DEV),
+                                       window_size=c["w"])
+    o_r, lse_r = oracle.decode_attention(q, k, v, lens.tolist(), full.tolist(),
+                                         window_size=c["w"])
+    _assert_close(o.unsqueeze(1), lse.unsqueeze(1), o_r.unsqueeze(1), lse_r.unsqueeze(1), tag=tag)
+
+
+@settings(max_examples=20, **SETTINGS)
+@given(c=st.fixed_dictionaries({
+    "s": st.integers(2, 600),
+    "hkv": st.integers(1, 2),
+    "g": st.sampled_from([1, 4, 5]),
+    "w": st.integers(1, 700),
+    "p": st.sampled_from([0.0, 0.3, 1.0]),
+    "cuts": st.lists(st.floats(0.02, 0.98), min_size=1, max_size=3),
+    "seed": st.integers(0, 2 ** 16),
+}))
+def test_split_merge_property(c):
+    """Keys cut into 2-4 chunks at random points: each chunk attended with
+    shard metadata, the partials merged by their log2 LSE, equals the
+    oracle on the whole key range."""
+    s, hkv = c["s"], c["hkv"]
+    hq = c["g"] * hkv
+    gen = torch.Generator().manual_seed(c["seed"])
+    q, k, v = workloads.make_qkv(gen, 1, s, s, hq, hkv, 128)
+    mask = torch.rand((1, s), generator=gen) < c["p"]
+    cuts = sorted({min(max(int(f * s), 1), s - 1) for f in c["cuts"]})
+    bounds = [0] + cuts + [s]
+    chunks = tuple(zip(bounds[:-1], bounds[1:]))
+    tag = f"split s{s} {hq}/{hkv} w{c['w']} p{c['p']} chunks{chunks} seed{c['seed']}"
+    print(f"[property] {tag}", flush=True)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    pos = torch.arange(s, dtype=torch.int32, device=DEV)
+    o, lse = _split_run(q.to(DEV), k.to(DEV), v.to(DEV), full, local, pos, chunks, c["w"])
+    f_ref, l_ref = R.compact(mask.reshape(-1).numpy())
+    o_r, lse_r = oracle.routed_attention(q, k, v, f_ref, l_ref, window_size=c["w"])
+    _assert_close(o, lse, o_r, lse_r, tag=tag)
+
