@@ -1,6 +1,6 @@
 """Property-based sweeps over small shapes (hypothesis): the HIP forward, the
-HIP backward, the compaction, the routed decode and split-then-merged key
-ranges against the CPU oracle.
+HIP backward, packed sequences (forward and backward), the compaction, the
+routed decode and split-then-merged key ranges against the CPU oracle.
 
 The examples are derandomized: every run draws the same fixed set of shapes
 (batch, lengths, head counts, group size, window, routing density, key
@@ -19,9 +19,10 @@ from hypothesis import strategies as st
 
 import oracle
 from oracle import routing as R
-from switchattentionkernels_amd import (build_switch_query_indices, switch_gqa_decode_forward,
+from switchattentionkernels_amd import (build_switch_attention_metadata,
+                                        build_switch_query_indices, switch_gqa_decode_forward,
                                         switch_gqa_prefill_backward, switch_gqa_prefill_forward,
-                                        workloads)
+                                        switch_gqa_prefill_varlen_forward, workloads)
 
 from test_gpu_parity import _assert_close, _split_run
 
@@ -168,4 +169,44 @@ def test_split_merge_property(c):
     f_ref, l_ref = R.compact(mask.reshape(-1).numpy())
     o_r, lse_r = oracle.routed_attention(q, k, v, f_ref, l_ref, window_size=c["w"])
     _assert_close(o, lse, o_r, lse_r, tag=tag)
+
+
+@settings(max_examples=20, **SETTINGS)
+@given(c=st.fixed_dictionaries({
+    "lens": st.lists(st.integers(1, 250), min_size=1, max_size=5),
+    "hkv": st.integers(1, 2),
+    "g": st.sampled_from([1, 4, 5, 8]),
+    "w": st.integers(1, 300),
+    "p": st.sampled_from([0.0, 0.3, 1.0]),
+    "seed": st.integers(0, 2 ** 16),
+}))
+def test_varlen_property(c):
+    """Packed sequences of random lengths (cu_seqlens): forward through
+    switch_gqa_prefill_varlen_forward and backward with the same metadata,
+    against the oracle on the restated per-segment bounds."""
+    cu = [0]
+    for n in c["lens"]:
+        cu.append(cu[-1] + n)
+    t, hkv = cu[-1], c["hkv"]
+    hq = c["g"] * hkv
+    gen = torch.Generator().manual_seed(c["seed"])
+    q, k, v = workloads.make_qkv(gen, 1, t, t, hq, hkv, 128)
+    mask = torch.rand((1, t), generator=gen) < c["p"]
+    do = torch.randn(q.shape, generator=gen).to(torch.bfloat16)
+    tag = f"varlen cu{cu} {hq}/{hkv} w{c['w']} p{c['p']} seed{c['seed']}"
+    print(f"[property] {tag}", flush=True)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_varlen_forward(qd, kd, vd, full, local, cu, window_size=c["w"])
+    md = build_switch_attention_metadata(t, t, device=DEV, window_size=c["w"], cu_seqlens=cu)
+    grads = switch_gqa_prefill_backward(qd, kd, vd, o, lse, do.to(DEV), full, local,
+                                        metadata=md, window_size=c["w"])
+    torch.cuda.synchronize()
+    ref_md = R.varlen_metadata(cu, cu, c["w"])
+    f_np, l_np = R.compact(mask.numpy())
+    o_ref, lse_ref = oracle.routed_attention(q, k, v, f_np, l_np, metadata=ref_md)
+    _assert_close(o, lse, o_ref, lse_ref, tag=tag)
+    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, metadata=ref_md)
+    for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
+        _grad_close(g, r, f"{tag} {name}")
 
