@@ -1,6 +1,7 @@
 """Property-based sweeps over small shapes (hypothesis): the HIP forward, the
-HIP backward, packed sequences (forward and backward), the compaction, the
-routed decode and split-then-merged key ranges against the CPU oracle.
+HIP backward, packed sequences (forward and backward), the compaction (from
+a mask and from router logits), the routed decode and split-then-merged key
+ranges against the CPU oracle.
 
 The examples are derandomized: every run draws the same fixed set of shapes
 (batch, lengths, head counts, group size, window, routing density, key
@@ -20,7 +21,9 @@ from hypothesis import strategies as st
 import oracle
 from oracle import routing as R
 from switchattentionkernels_amd import (build_switch_attention_metadata,
-                                        build_switch_query_indices, switch_gqa_decode_forward,
+                                        build_switch_query_indices,
+                                        build_switch_query_indices_from_logits,
+                                        switch_gqa_decode_forward,
                                         switch_gqa_prefill_backward, switch_gqa_prefill_forward,
                                         switch_gqa_prefill_varlen_forward, workloads)
 
@@ -104,6 +107,25 @@ def test_compaction_property(b, s, p, seed):
     flat = mask.reshape(-1)
     assert torch.equal(full.cpu(), torch.nonzero(flat).flatten().to(torch.int32))
     assert torch.equal(local.cpu(), torch.nonzero(~flat).flatten().to(torch.int32))
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(b=st.integers(1, 3), s=st.integers(1, 30000),
+       dtype=st.sampled_from([torch.float32, torch.bfloat16, torch.float16]),
+       thr=st.floats(-2.0, 2.0), special=st.floats(0.0, 0.05), seed=st.integers(0, 2 ** 16))
+def test_logits_compaction_property(b, s, dtype, thr, special, seed):
+    """Routing from logits in one pass equals thresholding then compacting,
+    bit for bit, with NaN and +-inf sprinkled in."""
+    gen = torch.Generator().manual_seed(seed)
+    lg = torch.randn((b, s), generator=gen) * 1.5
+    u = torch.rand((b, s), generator=gen)
+    lg[u < special / 3] = float("nan")
+    lg[(u >= special / 3) & (u < 2 * special / 3)] = float("inf")
+    lg[(u >= 2 * special / 3) & (u < special)] = float("-inf")
+    d = lg.to(dtype).to(DEV)
+    f, l = build_switch_query_indices_from_logits(d, thr)
+    f_ref, l_ref = build_switch_query_indices(d > thr)
+    assert torch.equal(f, f_ref) and torch.equal(l, l_ref), (b, s, dtype, thr, seed)
 
 
 @settings(max_examples=40, **SETTINGS)
