@@ -1,8 +1,8 @@
 """The entry points under HIP graph capture (torch.cuda.CUDAGraph).
 
 Nothing in the library synchronizes with the host, allocates, or records a
-memset, so a decode step or a prefill forward (on index lists that need no
-device check) can be captured once and replayed.  Each graph is replayed
+memset, so a decode step, a prefill forward or a forward and backward (on
+index lists that need no device check) can be captured once and replayed.  Each graph is replayed
 several times with new inputs written eagerly between replays, and every
 replay must equal an eager call on the same inputs bit for bit.  The decode
 replays also change the cache lengths and routing: its work split is planned
@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from switchattentionkernels_amd import (build_switch_query_indices, switch_gqa_decode_forward,
-                                        switch_gqa_prefill_forward)
+                                        switch_gqa_prefill_backward, switch_gqa_prefill_forward)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -70,3 +70,29 @@ def test_prefill_forward_graph_replays_match_eager():
         o_e, l_e = switch_gqa_prefill_forward(q, k, v, full, local, window_size=w)
         torch.cuda.synchronize()
         assert torch.equal(o_g, o_e) and torch.equal(l_g, l_e), f"prefill replay {i}"
+
+
+def test_prefill_forward_backward_graph_replays_match_eager():
+    s, hq, hkv, w = 1536, 16, 4, 300
+    g = torch.Generator(device=DEV).manual_seed(43)
+    q = torch.randn(1, s, hq, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(1, s, hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, s, hkv, 128, generator=g, device=DEV).to(torch.bfloat16)
+    do = torch.randn(1, s, hq, 128, generator=g, device=DEV).to(torch.bfloat16)
+    full, local = build_switch_query_indices(torch.rand(1, s, generator=g, device=DEV) < 0.4)
+
+    def step():
+        o, lse = switch_gqa_prefill_forward(q, k, v, full, local, window_size=w)
+        return (o, lse) + switch_gqa_prefill_backward(q, k, v, o, lse, do, full, local,
+                                                      window_size=w)
+
+    graph, outs_g = _capture(step)
+    for i in range(4):
+        for t in (q, k, do):
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(torch.bfloat16))
+        graph.replay()
+        outs_e = step()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("o", "lse", "dq", "dk", "dv"), outs_g, outs_e):
+            assert torch.equal(a, b), f"forward+backward replay {i}: {name}"
+
