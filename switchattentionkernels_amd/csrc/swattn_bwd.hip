@@ -92,11 +92,18 @@ struct BwdParams {
   uint16_t* qp;              // [blocks][32 rows][128]
   uint16_t* dop;
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
-  int32_t seq_q, seq_kv, total_kv, kv_tiles_dkv;
+  int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
   float scale;               // sm_scale
 };
+
+// A listed position outside [0, total_q) is never dereferenced: the host
+// checks the lists before the launch, and this keeps a list changed after
+// that check from turning into an out-of-bounds access.
+__device__ __forceinline__ bool pos_ok(const BwdParams& p, int pos) {
+  return static_cast<uint32_t>(pos) < static_cast<uint32_t>(p.total_q);
+}
 
 template <bool kMeta>
 __device__ __forceinline__ void row_bounds(const BwdParams& p, int branch, int pos, int& ks,
@@ -136,13 +143,17 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
   const int rr = tid >> 3, part = tid & 7;   // row in block, 16 d values per thread
   const int r = blk * kBRows + rr;
   const int G = p.group;
-  const bool valid = r < p.nrows[b];
+  bool valid = r < p.nrows[b];
   int pos = 0, qh = 0, ks = 0, ke = 0;
   if (valid) {
     const int slot = r / G;
     qh = kvh * G + (r - slot * G);
     pos = p.idx[b][slot];
-    row_bounds<kMeta>(p, b, pos, ks, ke);
+    valid = pos_ok(p, pos);   // otherwise a dead row: zeros, bounds [0, 0)
+    if (valid)
+      row_bounds<kMeta>(p, b, pos, ks, ke);
+    else
+      pos = 0;
   }
   const bool live = valid && ks < ke;
   uint4 qv[2], dv[2], ov[2];
@@ -219,7 +230,8 @@ __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p)
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     int ks, ke;
-    row_bounds<kMeta>(p, b, p.idx[b][mid], ks, ke);
+    const int pm = p.idx[b][mid];
+    row_bounds<kMeta>(p, b, pos_ok(p, pm) ? pm : 0, ks, ke);
     if (ke > k0) hi = mid; else lo = mid + 1;
   }
   const int s_lo = lo;
@@ -227,7 +239,8 @@ __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p)
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
     int ks, ke;
-    row_bounds<kMeta>(p, b, p.idx[b][mid], ks, ke);
+    const int pm = p.idx[b][mid];
+    row_bounds<kMeta>(p, b, pos_ok(p, pm) ? pm : 0, ks, ke);
     if (ks >= k1) hi = mid; else lo = mid + 1;
   }
   const int s_hi = lo;
@@ -674,11 +687,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     }
   }
 
-  if (valid) {
-    const int G = p.group;
-    const int slot = r / G;
-    const int qh = kvh * G + (r - slot * G);
-    const int pos = p.idx[b][slot];
+  const int G = p.group;
+  const int q_slot = r / G;
+  const int pos = valid ? p.idx[b][q_slot] : 0;
+  if (valid && pos_ok(p, pos)) {
+    const int qh = kvh * G + (r - q_slot * G);
     uint16_t* row = p.dq + (static_cast<int64_t>(pos) * p.hq + qh) * kD + 4 * h;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -821,6 +834,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.ranges = reinterpret_cast<int32_t*>(ws + L.off_ranges);
   p.seq_q = static_cast<int32_t>(seq_q);
   p.seq_kv = static_cast<int32_t>(seq_kv);
+  p.total_q = static_cast<int32_t>(total_q);
   p.total_kv = static_cast<int32_t>(total_kv);
   p.kv_tiles_dkv = static_cast<int32_t>(L.kv_tiles_dkv);
   p.hq = heads_q;

@@ -100,7 +100,7 @@ struct FwdParams {
   const uint16_t* vt;        // packed V^T tiles (vt_pack_kernel)
   int32_t count[2];
   int32_t tiles[2];
-  int32_t seq_q, seq_kv, total_kv, kv_tiles;
+  int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
 };
@@ -451,8 +451,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int r = tile * kRowsPerItem + wave * kRowsPerWave + rl;
   const int slot = r / G;
   const int qh = kvh * G + (r - slot * G);
-  const bool valid = slot < count;
-  const int pos = idx[valid ? slot : count - 1];
+  // A listed position outside [0, total_q) is treated like a padding row:
+  // nothing is read at it and nothing is stored for it.  The host checks the
+  // lists before the launch; this keeps a list changed after that check from
+  // turning into an out-of-bounds access.
+  const int listed = idx[slot < count ? slot : count - 1];
+  const bool in_range = static_cast<uint32_t>(listed) < static_cast<uint32_t>(p.total_q);
+  const bool valid = slot < count && in_range;
+  const int pos = in_range ? listed : 0;
   row_bounds<kMeta>(p, branch, pos, w.ks, w.ke);
   w.hh = hh;
   w.c = p.c;
@@ -619,6 +625,7 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
   p.tiles[1] = static_cast<int32_t>(ceil_div(n_local * group, kRowsPerItem));
   p.seq_q = static_cast<int32_t>(seq_q);
   p.seq_kv = static_cast<int32_t>(seq_kv);
+  p.total_q = static_cast<int32_t>(total_q);
   p.total_kv = static_cast<int32_t>(total_kv);
   p.kv_tiles = static_cast<int32_t>(kv_tiles_for(total_kv));
   p.hq = heads_q;

@@ -119,7 +119,13 @@ class _Compaction:
 def _tag_compacted(full: torch.Tensor, local: torch.Tensor, n: int) -> None:
     """Mark a fresh compaction result.  Both lists are ascending, disjoint and
     cover ``[0, n)`` by construction; torch's version counter (shared by the
-    two views of one buffer) shows whether either was modified since."""
+    two views of one buffer) shows whether either was modified since.
+
+    Inference tensors (made under ``torch.inference_mode()``) have no version
+    counter, so an in-place edit could not be seen: they are left untagged and
+    every forward call scans them in full."""
+    if full.is_inference():
+        return
     token = _Compaction(n)
     full._swattn_compaction = (token, "full", full._version)
     local._swattn_compaction = (token, "local", local._version)
@@ -130,6 +136,7 @@ def _is_untouched_compaction(full, local, seq_len: int) -> bool:
     b = getattr(local, "_swattn_compaction", None)
     return (a is not None and b is not None and a[0] is b[0] and a[0].n == seq_len
             and a[1] == "full" and b[1] == "local"
+            and not full.is_inference() and not local.is_inference()
             and full._version == a[2] and local._version == b[2])
 
 

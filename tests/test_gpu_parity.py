@@ -360,11 +360,17 @@ def test_s16k_config_sampled(p):
 
 
 def test_s64k_config_sampled():
+    """Config #5 on 1000+ rows, three quarters of them in the last quarter of
+    the sequence, where full routing is densest and full rows are longest."""
     wl = workloads.build("s64k", seed=4)
+    s = 65536
     o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
-    rows = _sample_rows(65536, 120, 4)
+    rng = np.random.default_rng(4)
+    tail = rng.choice(np.arange(3 * s // 4, s), 750, replace=False)
+    rows = np.unique(np.concatenate([_sample_rows(s, 250, 4), tail]))
+    assert rows.size >= 1000
     o_ref, lse_ref = _oracle(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"], rows=rows)
-    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag="config s64k")
+    _assert_close(o, lse, o_ref, lse_ref, rows=rows, tag=f"config s64k ({rows.size} rows)")
 
 
 # ----------------------------------------------------------------------------
