@@ -214,6 +214,27 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
                       size_t workspace_bytes, void* stream);
 
 /*
+ * swattn_decode_fwd without a workspace: the one entry point that allocates
+ * nothing and takes no scratch from the caller.  No counterpart in the
+ * reference.  It is for callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it.
+ * Same arguments, kernels and results as swattn_decode_fwd.  Its scratch is
+ * a library-owned device array of SWATTN_DECODE_NOALLOC_MAX_BYTES per GPU,
+ * held until the process ends; a shape whose
+ * swattn_decode_workspace_bytes() exceeds that is rejected (SWATTN_EINVAL,
+ * with a message).  Every call on one GPU shares that GPU's array: calls
+ * that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller.  The first call on each device looks up that
+ * device's array address (the device must be current, as for the launch).
+ */
+#define SWATTN_DECODE_NOALLOC_MAX_BYTES ((size_t)16 << 20)
+int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* cache_lens, const uint8_t* full, void* out,
+                              float* lse, int32_t batch, int64_t cache_len, int32_t heads_q,
+                              int32_t heads_kv, int32_t head_dim, int32_t window,
+                              float scale_log2, void* stream);
+
+/*
  * Routed GQA prefill backward: dq, dk, dv of swattn_prefill_fwd's output.
  * No counterpart in the reference, which is forward-only (V:14-15); this is
  * the derivative of its forward (V:103-249) and consumes the log2 LSE it

@@ -29,6 +29,8 @@ SIGNATURES = {
     "swattn_decode_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32,
                                          _i32, _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t,
                                          _vp]),
+    "swattn_decode_fwd_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64,
+                                                 _i32, _i32, _i32, _i32, ctypes.c_float, _vp]),
     "swattn_shard_bounds": (ctypes.c_int, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "swattn_merge_partials": (ctypes.c_int, [ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i32, _vp,
                                              _vp, _i64, _i32, _vp]),

@@ -19,6 +19,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -451,29 +452,35 @@ size_t swattn_decode_workspace_bytes(int32_t batch, int64_t cache_len, int32_t h
   return static_cast<size_t>(decode_layout(batch, heads_q, heads_kv, decode_cus()).bytes);
 }
 
-int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
-                      const int32_t* cache_lens, const uint8_t* full, void* out, float* lse,
-                      int32_t batch, int64_t cache_len, int32_t heads_q, int32_t heads_kv,
-                      int32_t head_dim, int32_t window, float scale_log2, void* workspace,
-                      size_t workspace_bytes, void* stream) {
-  if (head_dim != kD) return invalid("swattn_decode_fwd: head_dim must be 128");
-  if (batch < 1 || cache_len < 1 || heads_q < 1 || heads_kv < 1)
-    return invalid("swattn_decode_fwd: bad shape");
-  if (heads_q % heads_kv) return invalid("swattn_decode_fwd: heads_q must be a multiple of heads_kv");
-  const int group = heads_q / heads_kv;
-  if (group > kMaxG) return invalid("swattn_decode_fwd: heads_q / heads_kv must be at most 8");
-  if (window <= 0) return invalid("swattn_decode_fwd: window must be positive");
+}  // extern "C"
+
+// Argument checks shared by both decode entry points (name = the entry point).
+static int decode_check(const char* name, const void* q, const void* k_cache,
+                        const void* v_cache, const int32_t* cache_lens, const uint8_t* full,
+                        void* out, float* lse, int32_t batch, int64_t cache_len,
+                        int32_t heads_q, int32_t heads_kv, int32_t head_dim, int32_t window) {
+  const std::string n(name);
+  if (head_dim != kD) return invalid(n + ": head_dim must be 128");
+  if (batch < 1 || cache_len < 1 || heads_q < 1 || heads_kv < 1) return invalid(n + ": bad shape");
+  if (heads_q % heads_kv) return invalid(n + ": heads_q must be a multiple of heads_kv");
+  if (heads_q / heads_kv > kMaxG) return invalid(n + ": heads_q / heads_kv must be at most 8");
+  if (window <= 0) return invalid(n + ": window must be positive");
   if (batch > 65535 || heads_kv > 65535 || cache_len > INT32_MAX ||
       static_cast<int64_t>(batch) * heads_q > INT32_MAX)
-    return invalid("swattn_decode_fwd: batch, heads_kv or cache_len too large");
+    return invalid(n + ": batch, heads_kv or cache_len too large");
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr || cache_lens == nullptr ||
       full == nullptr || out == nullptr || lse == nullptr)
-    return invalid("swattn_decode_fwd: null pointer");
-  const size_t need = swattn_decode_workspace_bytes(batch, cache_len, heads_q, heads_kv);
-  if (workspace == nullptr || workspace_bytes < need) {
-    set_error("swattn_decode_fwd: workspace smaller than swattn_decode_workspace_bytes()");
-    return SWATTN_EWORKSPACE;
-  }
+    return invalid(n + ": null pointer");
+  return SWATTN_OK;
+}
+
+// Plan, split and merge kernels on `stream` with the (checked) workspace ws.
+static int decode_launch(const char* name, const void* q, const void* k_cache,
+                         const void* v_cache, const int32_t* cache_lens, const uint8_t* full,
+                         void* out, float* lse, int32_t batch, int64_t cache_len,
+                         int32_t heads_q, int32_t heads_kv, int32_t window, float scale_log2,
+                         char* ws, void* stream) {
+  const int group = heads_q / heads_kv;
   DecodeParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k_cache);
@@ -481,8 +488,7 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
   p.lens = cache_lens;
   p.full = full;
   const DecodeLayout L = decode_layout(batch, heads_q, heads_kv, decode_cus());
-  if (L.max_items > INT32_MAX) return invalid("swattn_decode_fwd: too many work items");
-  char* ws = static_cast<char*>(workspace);
+  if (L.max_items > INT32_MAX) return invalid(std::string(name) + ": too many work items");
   p.part_o = reinterpret_cast<float*>(ws);
   p.part_ml = reinterpret_cast<float*>(ws + L.off_ml);
   p.items = reinterpret_cast<int2*>(ws + L.off_items);
@@ -513,7 +519,95 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
   }
   const int64_t rows = static_cast<int64_t>(batch) * heads_q;
   hipLaunchKernelGGL(decode_merge_kernel, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, st, p);
-  return launch_status("swattn_decode_fwd");
+  return launch_status(name);
+}
+
+extern "C" {
+
+int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* cache_lens, const uint8_t* full, void* out, float* lse,
+                      int32_t batch, int64_t cache_len, int32_t heads_q, int32_t heads_kv,
+                      int32_t head_dim, int32_t window, float scale_log2, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  const char* name = "swattn_decode_fwd";
+  const int st = decode_check(name, q, k_cache, v_cache, cache_lens, full, out, lse, batch,
+                              cache_len, heads_q, heads_kv, head_dim, window);
+  if (st != SWATTN_OK) return st;
+  const size_t need = swattn_decode_workspace_bytes(batch, cache_len, heads_q, heads_kv);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("swattn_decode_fwd: workspace smaller than swattn_decode_workspace_bytes()");
+    return SWATTN_EWORKSPACE;
+  }
+  return decode_launch(name, q, k_cache, v_cache, cache_lens, full, out, lse, batch, cache_len,
+                       heads_q, heads_kv, window, scale_log2, static_cast<char*>(workspace),
+                       stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The same decode with library-owned scratch, for callers that cannot
+// allocate device memory (code under HIP graph capture, tight serving loops).
+// `scratch` is a file-scope device array: every GPU the library runs on gets
+// its own copy, held until the process ends.  In host code its name is only a
+// host-side stand-in, so its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// ever handed to kernels.  The decode kernels write every scratch byte they
+// read within the same call (plan, work items, split partials), so nothing
+// needs clearing between calls; two calls that overlap on one GPU share the
+// array and race.
+// ---------------------------------------------------------------------------
+constexpr size_t kDecodeScratchBytes = SWATTN_DECODE_NOALLOC_MAX_BYTES;   // 16 MiB per GPU
+static_assert(kDecodeScratchBytes % 256 == 0, "whole 256-byte lines");
+static __device__ __align__(256) char scratch[kDecodeScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];   // per device, nullptr until looked up
+
+// Device address of this GPU's scratch array (the current device's), or
+// nullptr with the error set.
+static void* scratch_for_current_device(const char* name) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    set_error(std::string(name) + ": no usable current device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error(std::string(name) + ": hipGetSymbolAddress(scratch): " + hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" {
+
+int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                              const int32_t* cache_lens, const uint8_t* full, void* out,
+                              float* lse, int32_t batch, int64_t cache_len, int32_t heads_q,
+                              int32_t heads_kv, int32_t head_dim, int32_t window,
+                              float scale_log2, void* stream) {
+  const char* name = "swattn_decode_fwd_noalloc";
+  const int st = decode_check(name, q, k_cache, v_cache, cache_lens, full, out, lse, batch,
+                              cache_len, heads_q, heads_kv, head_dim, window);
+  if (st != SWATTN_OK) return st;
+  const size_t need = swattn_decode_workspace_bytes(batch, cache_len, heads_q, heads_kv);
+  if (need > kDecodeScratchBytes) {
+    set_error("swattn_decode_fwd_noalloc: this shape needs " + std::to_string(need) +
+              " bytes of scratch, more than the library's " +
+              std::to_string(kDecodeScratchBytes) + " (use swattn_decode_fwd with a workspace)");
+    return SWATTN_EINVAL;
+  }
+  void* ws = scratch_for_current_device(name);
+  if (ws == nullptr) return SWATTN_EINVAL;
+  return decode_launch(name, q, k_cache, v_cache, cache_lens, full, out, lse, batch, cache_len,
+                       heads_q, heads_kv, window, scale_log2, static_cast<char*>(ws), stream);
 }
 
 }  // extern "C"

@@ -34,7 +34,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     funcs = _header_functions()
-    assert len(funcs) == 16, funcs
+    assert len(funcs) == 17, funcs
     lib = _lib.lib()
     for name in funcs:
         assert hasattr(lib, name), name

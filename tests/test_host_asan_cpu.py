@@ -69,6 +69,12 @@ CHILD = textwrap.dedent('''
                                              P, 1 << 30, None)
     err(dec(64, 8), EINVAL, "swattn_decode_fwd")
     err(dec(128, 32), EINVAL, "swattn_decode_fwd")     # group 16 > 8
+    dna = lambda b, hd, hq: L.swattn_decode_fwd_noalloc(P, P, P, P, P, P, P, b, 100, hq, 2, hd,
+                                                        64, 0.1, None)
+    err(dna(4, 64, 8), EINVAL, "swattn_decode_fwd_noalloc")
+    err(dna(4, 128, 32), EINVAL, "swattn_decode_fwd_noalloc")
+    err(dna(65535, 128, 16), EINVAL, "swattn_decode_fwd_noalloc")   # scratch too small
+    assert b"scratch" in L.swattn_last_error()
     err(L.swattn_shard_bounds(P, 10, 5, 2, 64, P, P, P, None), EINVAL, "swattn_shard_bounds")
     parts = (ctypes.c_void_p * 2)(P, None)
     lses = (ctypes.c_void_p * 2)(P, P)
