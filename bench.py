@@ -19,9 +19,13 @@ The JSON line also carries:
 * roofline: the attention kernel alone, timed with HIP events on the stream it
   runs on, against the 2516.6 TFLOP/s dense bf16 MFMA peak, and beside it the
   rate a register-only MFMA stream holds on this chip (swattn_mfma_peak);
+  ``traffic`` is copied from the committed rocprofv3 byte-counter summary
+  (``traffic_source`` says so), and ``gather_scatter`` is the rate of the
+  indexed Q reads and O / LSE writes over the kernel time;
 * cpu_baseline: the fp32 PyTorch oracle (a restatement of the reference's
   semantics -- the reference has no CPU path) on a bounded random row sample
-  of the same workload, on this host's cores;
+  of the same workload, on this host's cores (CPU model stated), and the
+  whole config #1 prefill (median of 10 after 2 warm-ups);
 * comparators: the same kernel on all-full routing (dense causal), torch
   SDPA causal (flash backend) on the same shape, the compaction alone, the
   routed decode extension (64 sequences, 8192-key caches) against HBM, and
@@ -142,6 +146,52 @@ def config_table(args):
             flush=True)
         del q, k, v, m, o, lse, do, full, local, md
         torch.cuda.empty_cache()
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _cpu_config1(seed: int) -> dict:
+    """The CPU timing planned for config #1 (B1 S1024 Hq8/Hkv2 W256, p_full
+    0.25): the whole oracle prefill, 2 warm-ups, median of 10."""
+    import numpy as np
+    import oracle
+    from oracle import routing as R
+    from switchattentionkernels_amd import workloads
+    wl = workloads.build("cpu", seed=seed)
+    f_np, l_np = R.compact(wl["mask"].numpy())
+    d = wl["workload"]
+    i = np.arange(d.seq_len)
+    is_full = np.zeros(d.seq_len, dtype=bool)
+    is_full[f_np] = True
+    pairs = int(np.where(is_full, i + 1, np.minimum(i + 1, d.window)).sum())
+    flops = 4 * 128 * d.heads_q * pairs
+
+    def run():
+        oracle.routed_attention(wl["q"], wl["k"], wl["v"], f_np, l_np, window_size=d.window)
+
+    times = []
+    with torch.inference_mode():
+        for it in range(12):
+            t0 = time.perf_counter()
+            run()
+            if it >= 2:
+                times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"workload": f"config #1: B1 S{d.seq_len} Hq{d.heads_q}/Hkv{d.heads_kv} d128 "
+                        f"W{d.window} p_full={d.p_full}, seed {seed}",
+            "ms_median_of_10": round(med * 1e3, 3), "routed_gflop": round(flops / 1e9, 3),
+            "gflops": round(flops / med / 1e9, 2), "threads": torch.get_num_threads(),
+            "method": "whole fp32 oracle prefill under inference_mode, 2 warm-ups, "
+                      "median of 10 (time.perf_counter)"}
 
 
 def decode_comparator(args, dev, HQ, HKV, D, W, iters, warmup):
@@ -361,17 +411,28 @@ def main():
     except Exception as exc:  # comparator only
         print(f"[bench] backward comparator unavailable: {exc}", file=sys.stderr, flush=True)
 
-    # ---- traffic (committed rocprofv3 --pmc result, if any) ---------------------
-    traffic = None
+    # ---- traffic: copied from the committed rocprofv3 --pmc summary, if any ------
+    # (byte counters cannot be read inside this timed run; the file states the
+    # command and the calibration that produced the figure)
+    traffic, traffic_src = None, None
     tpath = os.path.join(ROOT, "profiles", "fwd_s16k_p25_traffic.txt")
     if os.path.exists(tpath):
         for line in open(tpath):
             if line.startswith("traffic_bytes_per_launch"):
                 traffic = int(float(line.split("=")[1]))
+                traffic_src = ("copied from profiles/fwd_s16k_p25_traffic.txt (rocprofv3 --pmc "
+                               "FETCH_SIZE + WRITE_SIZE per launch, calibrated by a device copy); "
+                               "not measured in this run")
+
+    # ---- gather / scatter: Q rows read by index, O and LSE rows written by index ----
+    rows = B * S
+    gather_scatter_bytes = rows * HQ * D * 2 + rows * HQ * D * 2 + rows * HQ * 4 + rows * 4
 
     # ---- CPU baseline: the oracle on a bounded row sample -------------------------
     cpu = None
     if args.cpu_seconds > 0:
+        cpu_model = _cpu_model()
+        config1 = _cpu_config1(args.seed)
         import numpy as np
         import oracle
         from oracle import routing as R
@@ -406,7 +467,9 @@ def main():
                          f"{args.p_full} workload, fp32 dense-masked torch oracle, "
                          f"{t_cpu:.1f} s; host {os.cpu_count()} cpus, affinity "
                          f"{len(os.sched_getaffinity(0))}",
-               "ms_per_prefill_extrapolated": round(t_cpu * 1e3 * B * S / rows_done, 1)}
+               "cpu_model": cpu_model,
+               "ms_per_prefill_extrapolated": round(t_cpu * 1e3 * B * S / rows_done, 1),
+               "config1": config1}
 
     achieved = attn_tflops
     res = {
@@ -429,8 +492,19 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false>",
                      "kernel_ms": round(attn_ms, 4),
+                     "kernel_timing": f"HIP events on the launch stream around "
+                                      f"{max(args.steps, 50)} back-to-back calls after 10 "
+                                      f"warm-ups, in this run",
+                     "gather_scatter": {
+                         "bytes": gather_scatter_bytes,
+                         "what": "Q rows read and O / LSE rows written at their listed "
+                                 "positions, plus the index lists, over the kernel time",
+                         "gbs": round(gather_scatter_bytes / (attn_ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(gather_scatter_bytes / (attn_ms * 1e-3) / 1e9
+                                           / PEAK_HBM_GBS, 4)},
                      "achievable_mfma_tflops": None if mfma_tflops is None
                      else round(mfma_tflops, 1),
                      "frac_of_achievable": None if mfma_tflops is None
