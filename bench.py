@@ -18,7 +18,8 @@ pair).
 The JSON line also carries:
 * roofline: the attention kernel alone, timed with HIP events on the stream it
   runs on, against the 2516.6 TFLOP/s dense bf16 MFMA peak, and beside it the
-  rate a register-only MFMA stream holds on this chip (swattn_mfma_peak);
+  rate a register-only MFMA stream holds on this chip (swattn_mfma_peak, a
+  probe in its own library, libswattn_probe.so);
   ``traffic`` is copied from the committed rocprofv3 byte-counter summary
   (``traffic_source`` says so), and ``gather_scatter`` is the rate of the
   indexed Q reads and O / LSE writes over the kernel time;
@@ -356,10 +357,12 @@ def main():
         blocks, iters = 2 * cus, 20000
         probe = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
 
+        P = _lib.probe_lib()
+
         def peak():
-            st = L.swattn_mfma_peak(iters, blocks, probe.data_ptr(), stream)
+            st = P.swattn_mfma_peak(iters, blocks, probe.data_ptr(), stream)
             if st != 0:
-                raise RuntimeError(L.swattn_last_error().decode())
+                raise RuntimeError(f"swattn_mfma_peak failed with status {st}")
 
         peak_ms = time_launches(peak, 5, warmup=2)
         mfma_tflops = blocks * 4 * iters * 8 * 32768 / (peak_ms * 1e-3) / 1e12

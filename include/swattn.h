@@ -270,16 +270,6 @@ int swattn_prefill_bwd(const void* q, const void* k, const void* v, const void* 
                        int32_t head_dim, int32_t window, float scale_log2, void* workspace,
                        size_t workspace_bytes, void* stream);
 
-/*
- * Roofline diagnostic, no counterpart in the reference: `blocks` workgroups
- * of four waves each issue iters * 8 dependent-free v_mfma_f32_32x32x16_bf16
- * (32768 flop each) from registers, and each thread writes one float of
- * out[blocks * 256].  Timing it gives the bf16 matrix rate the chip holds
- * under a pure MFMA load (the clock drops below the one the published peak
- * assumes), against which the attention kernel's rate can be read.
- */
-int swattn_mfma_peak(int64_t iters, int32_t blocks, float* out, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

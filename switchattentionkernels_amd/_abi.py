@@ -42,13 +42,17 @@ SIGNATURES = {
     "swattn_prefill_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
                                           _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32,
                                           _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t, _vp]),
+}
+
+# libswattn_probe.so (bench.py's measurement probe; not part of swattn.h).
+PROBE_SIGNATURES = {
     "swattn_mfma_peak": (ctypes.c_int, [_i64, _i32, _vp, _vp]),
 }
 
 
-def bind(handle: ctypes.CDLL) -> ctypes.CDLL:
+def bind(handle: ctypes.CDLL, signatures=None) -> ctypes.CDLL:
     """Set restype / argtypes of every entry point on a loaded library."""
-    for name, (res, args) in SIGNATURES.items():
+    for name, (res, args) in (SIGNATURES if signatures is None else signatures).items():
         fn = getattr(handle, name)
         fn.restype = res
         fn.argtypes = args

@@ -14,13 +14,15 @@ import threading
 
 import torch  # noqa: F401  -- loads PyTorch's HIP runtime before the library
 
-from ._abi import SIGNATURES, bind  # noqa: F401  -- SIGNATURES is part of this module's API
+from ._abi import PROBE_SIGNATURES, SIGNATURES, bind  # noqa: F401  -- part of this module's API
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libswattn.so")
+PROBE_PATH = os.path.join(_HERE, "libswattn_probe.so")
 
 _lock = threading.Lock()
 _lib = None
+_probe = None
 
 
 class LibraryNotBuilt(RuntimeError):
@@ -40,6 +42,18 @@ def lib() -> ctypes.CDLL:
                     "`python -m switchattentionkernels_amd.build`")
             _lib = bind(ctypes.CDLL(LIB_PATH))
     return _lib
+
+
+def probe_lib() -> ctypes.CDLL:
+    """bench.py's measurement probe (``libswattn_probe.so``), loaded once."""
+    global _probe
+    with _lock:
+        if _probe is None:
+            if not os.path.exists(PROBE_PATH):
+                raise LibraryNotBuilt(f"{PROBE_PATH} is missing: build it with "
+                                      "`python -m switchattentionkernels_amd.build`")
+            _probe = bind(ctypes.CDLL(PROBE_PATH), PROBE_SIGNATURES)
+    return _probe
 
 
 def check(status: int, what: str) -> None:

@@ -22,7 +22,11 @@ LIB = os.path.join(HERE, "libswattn.so")
 ARCH = "gfx950"
 
 SOURCES = ["swattn_index.hip", "swattn_fwd.hip", "swattn_merge.hip", "swattn_decode.hip",
-           "swattn_bwd.hip", "swattn_diag.hip"]
+           "swattn_bwd.hip"]
+# The measurement probe bench.py uses, in a library of its own (not part of the
+# attention library's ABI).
+PROBE_SOURCES = ["probe/mfma_probe.hip"]
+PROBE_LIB = os.path.join(HERE, "libswattn_probe.so")
 
 
 def _hipcc() -> str:
@@ -63,14 +67,15 @@ def compile_flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False, out: str = LIB, extra_flags=()) -> str:
+def build(verbose: bool = False, out: str = LIB, extra_flags=(), sources=None) -> str:
     """Compile ``libswattn.so`` (or ``out``, with ``extra_flags`` appended to
-    the compile flags); returns its path.  Always recompiles."""
+    the compile flags; ``sources`` relative to ``csrc/``, default the
+    attention library's); returns its path.  Always recompiles."""
     cmd = [_hipcc()] + compile_flags() + list(extra_flags)
     tl = _torch_lib_dir()
     if tl is not None:
         cmd += ["-L", tl, "-Wl,-rpath," + tl]
-    cmd += [os.path.join(CSRC, s) for s in SOURCES]
+    cmd += [os.path.join(CSRC, s) for s in (SOURCES if sources is None else sources)]
     tmp = out + ".tmp"
     cmd += ["-o", tmp]
     if verbose:
@@ -86,5 +91,11 @@ def build(verbose: bool = False, out: str = LIB, extra_flags=()) -> str:
     return out
 
 
+def build_probe(verbose: bool = False) -> str:
+    """Compile ``libswattn_probe.so`` (bench.py's MFMA-rate probe)."""
+    return build(verbose=verbose, out=PROBE_LIB, sources=PROBE_SOURCES)
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_probe(verbose=True))

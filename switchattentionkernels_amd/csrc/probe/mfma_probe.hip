@@ -1,11 +1,18 @@
-// Roofline diagnostic for gfx950: the bf16 MFMA rate this chip sustains with
+// Measurement probe for gfx950, built as its own library (libswattn_probe.so)
+// and used only by bench.py: the bf16 MFMA rate this chip sustains with
 // nothing but v_mfma_f32_32x32x16_bf16 in flight (operands in registers, no
-// memory traffic, two waves per SIMD).  The attention kernel's
-// fraction of this rate separates scheduling losses from the clock the chip
-// holds under a full matrix-core load, which is below the one the published
-// peak assumes.  No counterpart in the reference.
+// memory traffic, two waves per SIMD).  The attention kernel's fraction of
+// this rate separates scheduling losses from the clock the chip holds under a
+// full matrix-core load, which is below the one the published peak assumes.
+// It is not part of the attention library's ABI (include/swattn.h).
+//
+//   int swattn_mfma_peak(int64_t iters, int32_t blocks, float* out, void* stream)
+//     blocks workgroups of 256 threads, each wave iters rounds of 8 MFMAs;
+//     out: blocks * 256 floats (written so the work is not optimised away).
+//     Returns 0, -1 for a bad argument, or a positive hipError_t.
 
-#include "common.h"
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace swattn {
 namespace {
@@ -45,9 +52,9 @@ __global__ __launch_bounds__(256) void mfma_peak_kernel(int64_t iters, float see
 using namespace swattn;
 
 extern "C" int swattn_mfma_peak(int64_t iters, int32_t blocks, float* out, void* stream) {
-  if (iters < 1 || blocks < 1) return invalid("swattn_mfma_peak: iters and blocks must be >= 1");
-  if (out == nullptr) return invalid("swattn_mfma_peak: null output");
+  if (iters < 1 || blocks < 1 || out == nullptr) return -1;
   hipLaunchKernelGGL(mfma_peak_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
-                     as_stream(stream), iters, 1e-3f, out);
-  return launch_status("swattn_mfma_peak");
+                     reinterpret_cast<hipStream_t>(stream), iters, 1e-3f, out);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : static_cast<int>(e);
 }

@@ -680,11 +680,12 @@ def test_decode_clamps_lengths_and_matches_prefill_last_row():
 
 
 def test_mfma_probe_runs_and_is_deterministic():
-    """The roofline probe is a diagnostic: it must launch cleanly and
-    every workgroup (same operands) must produce the same finite sums."""
-    L = _lib.lib()
+    """bench.py's roofline probe (libswattn_probe.so) is a diagnostic: it
+    must launch cleanly and every workgroup (same operands) must produce the
+    same finite sums."""
+    P = _lib.probe_lib()
     out = torch.empty(3 * 256, dtype=torch.float32, device=DEV)
-    assert L.swattn_mfma_peak(100, 3, out.data_ptr(), _lib.stream_handle(out.device)) == 0
+    assert P.swattn_mfma_peak(100, 3, out.data_ptr(), _lib.stream_handle(out.device)) == 0
     r = out.view(3, 256).cpu()
     assert torch.isfinite(r).all() and (r != 0).any()
     assert torch.equal(r[0], r[1]) and torch.equal(r[0], r[2])

@@ -82,7 +82,6 @@ CHILD = textwrap.dedent('''
         "swattn_merge_partials")
     err(L.swattn_merge_partials(parts, lses, 17, P, P, 10, 128, None), EINVAL,
         "swattn_merge_partials")
-    err(L.swattn_mfma_peak(0, 4, P, None), EINVAL, "swattn_mfma_peak")
     print("host checks ok")
 ''')
 
