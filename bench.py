@@ -518,6 +518,8 @@ def main():
             "routed_flop_fraction": round(flops / dense_flops, 4),
             "routed_over_dense_time": round(attn_ms / dense_ms, 4),
             "sdpa_flash_causal_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
+            "routed_over_sdpa_dense_time": None if sdpa_ms is None
+            else round(attn_ms / sdpa_ms, 4),
             "compaction_us": round(compact_ms * 1e3, 2),
             "compaction_gbs": round(compact_bytes / (compact_ms * 1e-3) / 1e9, 1),
             "compaction_logits_us": round(logits_ms * 1e3, 2),
