@@ -5,7 +5,9 @@
  * Every entry point takes device pointers, plain sizes and a hipStream_t
  * (passed as void*; NULL = the legacy default stream), enqueues its kernels on
  * that stream and returns without synchronising.  Nothing here allocates
- * device memory: scratch space is passed in by the caller.
+ * device memory: scratch space is passed in by the caller.  bf16 row tensors
+ * (q, k, v, out and their gradients, KV caches, merge partials) must be
+ * 16-byte aligned; a misaligned one is rejected with SWATTN_EINVAL.
  *
  * Return value: SWATTN_OK (0) on success, a negative SWATTN_E* code for an
  * invalid argument detected on the host, or a positive hipError_t from the
@@ -251,8 +253,10 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *   dq         bf16 like q: rows listed in full_idx/local_idx are written,
  *              others untouched; a row with no legal key gets 0.
  *   dk, dv     bf16 like k: every key row is written (0 where no row sees it).
- *   workspace  >= swattn_prefill_bwd_workspace_bytes(...) (depends on the
- *              list lengths); overwritten (calls sharing it must not overlap).
+ *   workspace  >= swattn_prefill_bwd_workspace_bytes(...): 1 KiB of row
+ *              info per KV head and 32 listed rows, plus a little (Q and dO
+ *              are read in place, never copied); overwritten (calls sharing
+ *              it must not overlap).
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
  * ascending positions): the keys a row block can see are found by binary

@@ -30,6 +30,11 @@ inline int invalid(const std::string& msg) {
   return SWATTN_EINVAL;
 }
 
+// bf16 row tensors (Q, K, V, O and their gradients, caches, partials) move
+// in 16-byte pieces, by vector loads and global -> LDS DMAs: their base
+// pointers must be 16-byte aligned.
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // popcount(mask & lanes_below_me) without a lane-mask table.
 __device__ __forceinline__ int count_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),

@@ -12,18 +12,22 @@
 // with dk_j / dv_j summed over the G query heads of the KV head.
 //
 // Design (MI355X-first):
-// * Rows are packed as in the forward (compacted query slot, head of the
+// * Rows are ordered as in the forward (compacted query slot, head of the
 //   group; head fastest), in blocks of 32.  bwd_prep_kernel computes Delta
-//   once per row and writes, per (branch, KV head, block), Q and dO as
-//   row-major 8 KiB blocks plus a 1 KiB block of row info (LSE, Delta, key
-//   bounds, and the block's bounds summary).
+//   once per row and writes, per (branch, KV head, block), a 1 KiB block of
+//   row info: LSE, Delta, key bounds, the block's bounds summary, and each
+//   row's element offset in Q / dO (-1 for a row that contributes nothing).
+//   Q and dO themselves are never copied.
 // * bwd_dkdv_kernel: one workgroup of eight waves (two per SIMD) per
 //   (256-key tile, KV head); each wave keeps its 32 keys' K as MFMA B
 //   operands in registers and dK^T, dV^T (128 d x 32 keys each) in
 //   accumulators; the workgroup's V rows sit in LDS.  It streams the row
 //   blocks that can see the tile (a contiguous block range per branch,
 //   found by bwd_ranges_kernel with a binary search over the monotone row
-//   bounds) through a three-slot LDS ring filled by buffer_load ... lds.
+//   bounds) through a three-slot LDS ring.  Each block's 32 Q and dO rows
+//   are gathered from their positions by global_load_lds_dwordx4 (one
+//   64-bit source address per lane), from the row offsets of the block's
+//   info, which travels one block ahead through a four-slot info ring.
 //   Four MFMA products per block: S = Q K^T, dP = dO V^T, dV^T += dO^T P,
 //   dK^T += Q^T dS.  The A operands of the last two (Q^T, dO^T) come from
 //   the same row-major blocks through transposing LDS reads
@@ -31,11 +35,11 @@
 //   order the S / dP accumulators hold them, so those accumulators are the
 //   B operands unchanged.
 // * bwd_dq_kernel: one workgroup of eight waves per (branch, 256-row tile,
-//   KV head), the forward's shape: each wave owns 32 rows, keeps Q^T and
-//   dO^T as B operands, and streams K and V tiles through a three-slot LDS
-//   ring.  Three products per 64-key tile: S^T = K Q^T, dP^T = V dO^T,
-//   dQ^T += K^T dS^T (K^T by transposing reads of the K tile; dS^T as B
-//   operand straight from the accumulator).
+//   KV head), the forward's shape: each wave owns 32 rows, loads Q^T and
+//   dO^T from the rows' positions as B operands, and streams K and V tiles
+//   through a three-slot LDS ring.  Three products per 64-key tile: S^T =
+//   K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T (K^T by transposing reads of
+//   the K tile; dS^T as B operand straight from the accumulator).
 // * Keys outside a row's range get S = -inf, so P = 0 exactly; a row with no
 //   legal key (or a padding row) carries LSE = Delta = 0 and bounds [0, 0),
 //   is masked everywhere and contributes nothing.
@@ -55,18 +59,22 @@ using namespace tiles;
 constexpr int kThreads = 256;                          // prep / ranges workgroups
 constexpr int kBwdWaves = 8;                           // dK/dV and dQ: two waves per SIMD
 constexpr int kBwdThreads = kBwdWaves * 64;
-constexpr int kBRows = 32;                             // rows per packed block
-constexpr int kBlockBytes = kBRows * kRowBytes;        // 8 KiB row-major or transposed block
+constexpr int kBRows = 32;                             // rows per block
+constexpr int kBlockBytes = kBRows * kRowBytes;        // 8 KiB row-major block in LDS
 constexpr int kInfoBytes = 1024;                       // row info block
 constexpr int kInfoLse = 0, kInfoDelta = 32, kInfoStart = 64, kInfoEnd = 96;   // word offsets
 constexpr int kInfoMaxStart = 128, kInfoMinEnd = 129;
+constexpr int kInfoRowOff = 96;                        // int64 offset: row element offsets (bytes 768..1023)
 constexpr int kKeysDkv = kBwdWaves * 32;               // keys per dK/dV workgroup (32 per wave)
 constexpr int kRowsPerItem = kBwdWaves * 32;           // rows per dQ workgroup (32 per wave)
 constexpr int kVTileBytes = kKeysDkv * kRowBytes;      // the dK/dV workgroup's V rows: 64 KiB
-// dK/dV LDS ring slot: Q block, dO block (row-major), info; three slots.
-constexpr int kStageBytes = 2 * kBlockBytes + kInfoBytes;
-constexpr int kOffQ = 0, kOffDO = kBlockBytes, kOffInfo = 2 * kBlockBytes;
+// dK/dV LDS ring slot: Q block, dO block (row-major); three slots.  The
+// blocks' info goes through its own four-slot ring, one block ahead.
+constexpr int kStageBytes = 2 * kBlockBytes;
+constexpr int kOffQ = 0, kOffDO = kBlockBytes;
 constexpr int kRingSlots = 3;
+constexpr int kInfoSlots = 4;
+constexpr int kDkvLdsBytes = kVTileBytes + kRingSlots * kStageBytes + kInfoSlots * kInfoBytes;
 // dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
 constexpr int kQStageBytes = 2 * kTileBytes;
 
@@ -89,8 +97,7 @@ struct BwdParams {
   int32_t items[2];          // ceil(nrows / 128)
   int64_t blk_base[2];       // packed block of (branch b, head h, block i): blk_base[b] + h * blocks[b] + i
   char* info;                // [blocks][1 KiB]
-  uint16_t* qp;              // [blocks][32 rows][128]
-  uint16_t* dop;
+  uint16_t* zero_row;        // 128 zeros: the gather source of rows that contribute nothing
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
   int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
@@ -156,16 +163,15 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
       pos = 0;
   }
   const bool live = valid && ks < ke;
-  uint4 qv[2], dv[2], ov[2];
+  const int64_t row_off = (static_cast<int64_t>(pos) * p.hq + qh) * kD;
+  uint4 dv[2], ov[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) qv[i] = dv[i] = ov[i] = make_uint4(0, 0, 0, 0);
-  if (valid) {
-    const int64_t off = (static_cast<int64_t>(pos) * p.hq + qh) * kD + 16 * part;
+  for (int i = 0; i < 2; ++i) dv[i] = ov[i] = make_uint4(0, 0, 0, 0);
+  if (live) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      qv[i] = *reinterpret_cast<const uint4*>(p.q + off + 8 * i);
-      dv[i] = *reinterpret_cast<const uint4*>(p.dout + off + 8 * i);
-      ov[i] = *reinterpret_cast<const uint4*>(p.o + off + 8 * i);
+      dv[i] = *reinterpret_cast<const uint4*>(p.dout + row_off + 16 * part + 8 * i);
+      ov[i] = *reinterpret_cast<const uint4*>(p.o + row_off + 16 * part + 8 * i);
     }
   }
   float delta = 0.f;
@@ -183,13 +189,9 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
   delta += __shfl_xor(delta, 2);
   delta += __shfl_xor(delta, 4);
 
-  uint16_t* qp = p.qp + pb * (kBlockBytes / 2) + rr * kD + 16 * part;
-  uint16_t* dop = p.dop + pb * (kBlockBytes / 2) + rr * kD + 16 * part;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    *reinterpret_cast<uint4*>(qp + 8 * i) = qv[i];
-    *reinterpret_cast<uint4*>(dop + 8 * i) = dv[i];
-  }
+  // The gather source of every row that contributes nothing.
+  if (x == 0 && kvh == 0 && tid < kRowBytes / 16)
+    reinterpret_cast<uint4*>(p.zero_row)[tid] = make_uint4(0, 0, 0, 0);
   if (part == 0) {
     float* inf = reinterpret_cast<float*>(p.info + pb * kInfoBytes);
     int* infi = reinterpret_cast<int*>(inf);
@@ -197,6 +199,7 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
     inf[kInfoDelta + rr] = live ? delta : 0.f;
     infi[kInfoStart + rr] = live ? ks : 0;
     infi[kInfoEnd + rr] = live ? ke : 0;
+    reinterpret_cast<int64_t*>(inf)[kInfoRowOff + rr] = live ? row_off : -1;
     s_ks[rr] = live ? ks : INT_MAX;   // a dead row forces the mask on its block
     s_ke[rr] = live ? ke : INT_MIN;
   }
@@ -258,23 +261,26 @@ __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p)
 // dK / dV: one workgroup per (256-key tile, KV head), eight waves of 32 keys.
 // ---------------------------------------------------------------------------
 struct DkvPlan {
-  uint32_t off[2];   // this lane's source offset inside its block part, per 1 KiB load
+  int row[2];        // this lane's block row, per 1 KiB load
+  uint32_t cb[2];    // byte offset inside that row of the chunk this lane fetches
   uint32_t voff[8];  // V rows: source offset from the tile's first key row, per 1 KiB load
 };
 
 // Waves 4p .. 4p+3 stage the four quarters of block part p (0 = Q, 1 = dO;
 // row-major 256-byte rows, chunk swizzle swz): lane l of load i lands on
-// byte 16 c of the part, c = 128 quarter + 64 i + l, and fetches the logical
-// chunk that belongs there.  The V tile (256 key rows, swizzle swz) is
-// staged once: wave w loads rows 32w .. 32w+31, four rows per load.
+// byte 16 c of the part, c = 128 quarter + 64 i + l, i.e. on chunk position
+// c % 16 of block row c / 16, and fetches the logical chunk that belongs
+// there from that row's position in Q or dO.  The V tile (256 key rows,
+// swizzle swz) is staged once: wave w loads rows 32w .. 32w+31, four rows
+// per load.
 __device__ __forceinline__ DkvPlan make_dkv_plan(const BwdParams& p, int kvh, int wave, int lane) {
   DkvPlan pl;
   const int quarter = wave & 3;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int c = 128 * quarter + 64 * i + lane;
-    const int row = c >> 4;
-    pl.off[i] = static_cast<uint32_t>(row * kRowBytes + (((c & 15) ^ swz(row)) << 4));
+    pl.row[i] = c >> 4;
+    pl.cb[i] = static_cast<uint32_t>(((c & 15) ^ swz(c >> 4)) << 4);
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -285,19 +291,29 @@ __device__ __forceinline__ DkvPlan make_dkv_plan(const BwdParams& p, int kvh, in
   return pl;
 }
 
-// Two 1 KiB loads per wave, plus the 1 KiB info block from the last wave.
-__device__ __forceinline__ void stage_dkv(const BwdParams& p, const DkvPlan& pl, int wave,
-                                          int lane, int64_t pb, uint32_t slot) {
+// A block's Q and dO rows: two 1 KiB gathers per wave into the ring slot at
+// LDS address slot, from the row offsets of the block's info (already in
+// LDS at info).  A row with offset -1 is fetched from the zero row.
+__device__ __forceinline__ void stage_rows(const BwdParams& p, const DkvPlan& pl, int wave,
+                                           const char* info, uint32_t slot) {
   const int part = wave >> 2, quarter = wave & 3;
-  const uint16_t* src = part == 0 ? p.qp : p.dop;
-  const i32x4 rs = make_rsrc(src + pb * (kBlockBytes / 2), kBlockBytes);
+  const char* src = reinterpret_cast<const char*>(part == 0 ? p.q : p.dout);
+  const int64_t* row_off = reinterpret_cast<const int64_t*>(info) + kInfoRowOff;
   const uint32_t dst = slot + part * kBlockBytes + quarter * (kBlockBytes / 4);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) dma16(rs, pl.off[i], __builtin_amdgcn_readfirstlane(dst + 1024 * i));
-  if (wave == kBwdWaves - 1) {
-    const i32x4 ri = make_rsrc(p.info + pb * kInfoBytes, kInfoBytes);
-    dma16(ri, static_cast<uint32_t>(16 * lane), __builtin_amdgcn_readfirstlane(slot + kOffInfo));
+  for (int i = 0; i < 2; ++i) {
+    const int64_t ro = row_off[pl.row[i]];
+    const char* a = (ro >= 0 ? src + 2 * ro : reinterpret_cast<const char*>(p.zero_row)) + pl.cb[i];
+    dma16_gather(a, __builtin_amdgcn_readfirstlane(dst + 1024 * i));
   }
+}
+
+// A block's 1 KiB info into the info ring slot at LDS address slot (one
+// load, issued by the last wave; the same load form as the row gathers, so
+// that the loop's vmcnt counts cover one kind of load).
+__device__ __forceinline__ void stage_info(const BwdParams& p, int lane, int64_t pb,
+                                           uint32_t slot) {
+  dma16_gather(p.info + pb * kInfoBytes + 16 * lane, __builtin_amdgcn_readfirstlane(slot));
 }
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -323,8 +339,8 @@ __device__ __forceinline__ bf16x8 read_xt(const char* xb, int off0, int off1) {
 
 __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
                           amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_kernel(const BwdParams p) {
-  // [V tile: 256 key rows][three block slots]
-  __shared__ __attribute__((aligned(1024))) char smem[kVTileBytes + kRingSlots * kStageBytes];
+  // [V tile: 256 key rows][three Q / dO block slots][four info slots]
+  __shared__ __attribute__((aligned(1024))) char smem[kDkvLdsBytes];
   const int tid = threadIdx.x;
   // The wave index as a scalar: per-wave choices (which block part a wave
   // stages, its source pointer) then stay scalar selects.
@@ -365,6 +381,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   const DkvPlan pl = make_dkv_plan(p, kvh, wave, lane);
   const uint32_t lds0 = lds_addr(smem);
   const uint32_t ring0 = lds0 + kVTileBytes;
+  const uint32_t info0 = ring0 + kRingSlots * kStageBytes;
+  const char* info_lds = smem + kVTileBytes + kRingSlots * kStageBytes;
   // The V tile, once: rows past total_kv fall outside the descriptor.
   if (nb > 0) {
     const int64_t row_bytes = static_cast<int64_t>(p.hkv) * kD * 2;
@@ -392,30 +410,42 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
   const char* vrow = smem + 32 * wave * kRowBytes;
 
-  // Three-slot ring: block i+2 loads while block i is computed.
-  if (nb > 0) stage_dkv(p, pl, wave, lane, block_of(0), ring0);
-  if (nb > 1) stage_dkv(p, pl, wave, lane, block_of(1), ring0 + kStageBytes);
+  // Three-slot row ring: block i+2's rows load while block i is computed;
+  // the four-slot info ring runs one block further ahead (block i+3), so
+  // that a block's row offsets are in LDS when its rows are gathered.  The
+  // prologue stages the info of blocks 0..2 and, once it has landed, the
+  // rows of blocks 0 and 1.  (The other waves' V loads may stay in flight:
+  // block 0's wait covers them.)
+  if (wave == kBwdWaves - 1) {
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+      if (j < nb) stage_info(p, lane, block_of(j), info0 + j * kInfoBytes);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  asm volatile("s_barrier" ::: "memory");
+  if (nb > 0) stage_rows(p, pl, wave, info_lds, ring0);
+  if (nb > 1) stage_rows(p, pl, wave, info_lds + kInfoBytes, ring0 + kStageBytes);
   int slot = 0;
   for (int i = 0; i < nb; ++i) {
-    // Block i (and, before block 0, the V tile) is in LDS once every wave's
-    // own loads up to it are complete (block i+1's may stay in flight: two
-    // loads, three for the last wave); every wave has finished block i-1,
-    // whose slot the next loads overwrite.
-    if (i + 1 < nb) {
-      if (wave == kBwdWaves - 1)
-        asm volatile("s_waitcnt vmcnt(3) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    } else {
+    // Block i's rows (and, before block 0, the V tile) are in LDS once every
+    // wave's own loads up to them are complete.  Only block i+1's two row
+    // gathers, the last loads a wave issued, may stay in flight; the info of
+    // block i+2, issued before them, has landed.  Every wave has finished
+    // block i-1, whose row slot and info slot the next loads overwrite.
+    if (i + 1 < nb)
+      asm volatile("s_waitcnt vmcnt(2) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    }
+    if (wave == kBwdWaves - 1 && i + 3 < nb)
+      stage_info(p, lane, block_of(i + 3), info0 + ((i + 3) & 3) * kInfoBytes);
     if (i + 2 < nb) {
       const int s2slot = slot >= 1 ? slot - 1 : slot + 2;   // (i + 2) % 3
-      stage_dkv(p, pl, wave, lane, block_of(i + 2), ring0 + s2slot * kStageBytes);
+      stage_rows(p, pl, wave, info_lds + ((i + 2) & 3) * kInfoBytes,
+                 ring0 + s2slot * kStageBytes);
     }
     const char* sb = smem + kVTileBytes + slot * kStageBytes;
     slot = slot == kRingSlots - 1 ? 0 : slot + 1;
-    const float* inf = reinterpret_cast<const float*>(sb + kOffInfo);
+    const float* inf = reinterpret_cast<const float*>(info_lds + (i & 3) * kInfoBytes);
     const int* infi = reinterpret_cast<const int*>(inf);
 
     f32x16 s = f32x16{}, dp = f32x16{};
@@ -547,8 +577,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   const int r = blk * kBRows + n;
   const bool valid = blk_ok && r < p.nrows[b];
 
+  // The row's element offset in Q / dO (-1: the row contributes nothing, its
+  // operands are zeros and its bounds empty).
   float lse = 0.f, delta = 0.f;
   int ks = 0, ke = 0;
+  int64_t row_off = -1;
   bf16x8 qf[8], dof[8];
   if (valid) {
     const float* inf = reinterpret_cast<const float*>(p.info + pb * kInfoBytes);
@@ -557,8 +590,11 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     delta = inf[kInfoDelta + n];
     ks = infi[kInfoStart + n];
     ke = infi[kInfoEnd + n];
-    const uint16_t* qrow = p.qp + pb * (kBlockBytes / 2) + n * kD + 8 * h;
-    const uint16_t* drow = p.dop + pb * (kBlockBytes / 2) + n * kD + 8 * h;
+    row_off = reinterpret_cast<const int64_t*>(inf)[kInfoRowOff + n];
+  }
+  if (row_off >= 0) {
+    const uint16_t* qrow = p.q + row_off + 8 * h;
+    const uint16_t* drow = p.dout + row_off + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
       qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
@@ -711,7 +747,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // ---------------------------------------------------------------------------
 struct BwdLayout {
   int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv;
-  size_t off_info, off_qp, off_dop, off_ranges, bytes;
+  size_t off_info, off_zero, off_ranges, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -728,8 +764,7 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   L.kv_tiles_dkv = ceil_div(total_kv, kKeysDkv);
   size_t o = 0;
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
-  L.off_qp = o;     o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
-  L.off_dop = o;    o = align256(o + static_cast<size_t>(L.total_blocks) * kBlockBytes);
+  L.off_zero = o;   o = align256(o + kRowBytes);
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.bytes = o;
   return L;
@@ -794,6 +829,10 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
       (q == nullptr || out == nullptr || lse == nullptr || dout == nullptr || dq == nullptr ||
        (n_full > 0 && full_idx == nullptr) || (n_local > 0 && local_idx == nullptr)))
     return invalid("swattn_prefill_bwd: null pointer");
+  if (!aligned16(k) || !aligned16(v) || !aligned16(dk) || !aligned16(dv) ||
+      (n_full + n_local > 0 &&
+       (!aligned16(q) || !aligned16(out) || !aligned16(dout) || !aligned16(dq))))
+    return invalid("swattn_prefill_bwd: q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
   const BwdLayout L = bwd_layout(total_kv, heads_kv, group, n_full, n_local);
   if (workspace == nullptr || workspace_bytes < L.bytes) {
     set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
@@ -829,8 +868,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.blk_base[0] = 0;
   p.blk_base[1] = static_cast<int64_t>(heads_kv) * L.blocks[0];
   p.info = ws + L.off_info;
-  p.qp = reinterpret_cast<uint16_t*>(ws + L.off_qp);
-  p.dop = reinterpret_cast<uint16_t*>(ws + L.off_dop);
+  p.zero_row = reinterpret_cast<uint16_t*>(ws + L.off_zero);
   p.ranges = reinterpret_cast<int32_t*>(ws + L.off_ranges);
   p.seq_q = static_cast<int32_t>(seq_q);
   p.seq_kv = static_cast<int32_t>(seq_kv);

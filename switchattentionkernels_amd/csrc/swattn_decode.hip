@@ -471,6 +471,8 @@ static int decode_check(const char* name, const void* q, const void* k_cache,
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr || cache_lens == nullptr ||
       full == nullptr || out == nullptr || lse == nullptr)
     return invalid(n + ": null pointer");
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return invalid(n + ": q, k_cache, v_cache and out must be 16-byte aligned");
   return SWATTN_OK;
 }
 

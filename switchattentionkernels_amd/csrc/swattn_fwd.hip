@@ -601,6 +601,8 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || lse == nullptr ||
       (n_full > 0 && full_idx == nullptr) || (n_local > 0 && local_idx == nullptr))
     return invalid("swattn_prefill_fwd: null pointer");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return invalid("swattn_prefill_fwd: q, k, v and out must be 16-byte aligned");
   const size_t ws_need = swattn_prefill_workspace_bytes(batch, seq_kv, heads_kv, head_dim);
   if (workspace == nullptr || workspace_bytes < ws_need) {
     set_error("swattn_prefill_fwd: workspace smaller than swattn_prefill_workspace_bytes()");

@@ -134,10 +134,14 @@ int swattn_merge_partials(const void* const* o_parts, const float* const* lse_pa
   for (int i = 0; i < n_parts; ++i) {
     if (o_parts[i] == nullptr || lse_parts[i] == nullptr)
       return invalid("swattn_merge_partials: null part");
+    if (!aligned16(o_parts[i]))
+      return invalid("swattn_merge_partials: partial outputs and out must be 16-byte aligned");
     a.o[i] = static_cast<const uint16_t*>(o_parts[i]);
     a.lse[i] = lse_parts[i];
   }
   a.parts = n_parts;
+  if (!aligned16(out))
+    return invalid("swattn_merge_partials: partial outputs and out must be 16-byte aligned");
   const int64_t blocks = ceil_div(rows * 16, 256);
   if (blocks > INT32_MAX) return invalid("swattn_merge_partials: too many rows");
   hipLaunchKernelGGL(merge_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,

@@ -1,7 +1,8 @@
 // Tile layouts and data movement shared by the gfx950 attention kernels
 // (forward and backward): operand vector types, the LDS chunk swizzles, the
 // key-permutation inside 16-key groups, raw buffer descriptors, the
-// global -> LDS DMA, and the V^T (or K^T) tile packer.
+// global -> LDS DMA (buffer-descriptor and per-lane gather forms), and the
+// V^T (or K^T) tile packer.
 #pragma once
 
 #include "common.h"
@@ -85,6 +86,15 @@ __device__ __forceinline__ void dma16(const i32x4& rsrc, uint32_t voff, uint32_t
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(lds_base)
+               : "memory", "m0");
+}
+// 16 bytes per lane from the 64-bit global address src to LDS at lds_base +
+// 16 * lane (global_load_lds_dwordx4, gfx950): a gather with one source row
+// per lane and no 4 GiB window.  Issued and waited for like dma16.
+__device__ __forceinline__ void dma16_gather(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
 __device__ __forceinline__ uint32_t lds_addr(const char* p) {

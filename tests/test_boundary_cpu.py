@@ -52,10 +52,11 @@ def test_version_and_workspace():
     # V^T tiles: Hkv x ceil(B*Skv / 64) x 16 KiB
     assert lib.swattn_prefill_workspace_bytes(2, 100, 8, 128) == 8 * 4 * 16384
     assert lib.swattn_prefill_workspace_bytes(1, 100, 8, 64) == 0
-    # backward: per KV head and 32-row block 1 KiB of row info + two 8 KiB
-    # Q / dO blocks, and 256-key block ranges (256-byte aligned).
+    # backward: per KV head and 32-row block 1 KiB of row info (Q and dO are
+    # gathered in place, never copied), one 256-byte zero row, and 256-key
+    # block ranges (256-byte aligned).
     nb = 8 * (-(-(300 * 4) // 32) + -(-(700 * 4) // 32))
-    expect = nb * 1024 + 2 * nb * 8192 + 256
+    expect = nb * 1024 + 256 + 256
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 128, 300, 700) == expect
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 30, 8, 128, 300, 700) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 64, 300, 700) == 0

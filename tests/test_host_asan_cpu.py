@@ -82,6 +82,29 @@ CHILD = textwrap.dedent('''
         "swattn_merge_partials")
     err(L.swattn_merge_partials(parts, lses, 17, P, P, 10, 128, None), EINVAL,
         "swattn_merge_partials")
+    # bf16 row tensors must be 16-byte aligned (a bf16 view can be 2-aligned)
+    M = P + 2
+    def unaligned(rc, name):
+        err(rc, EINVAL, name)
+        assert b"16-byte aligned" in L.swattn_last_error(), L.swattn_last_error()
+    unaligned(L.swattn_prefill_fwd(P, M, P, P, 100, P, 100, None, None, None, P, P, 1, 200, 200,
+                                   32, 8, 128, 64, 0.1, P, 1 << 30, None), "swattn_prefill_fwd")
+    unaligned(L.swattn_prefill_bwd(P, P, P, P, P, M, P, 100, P, 100, None, None, None, P, P, P,
+                                   1, 200, 200, 32, 8, 128, 64, 0.1, P, wsb, None),
+              "swattn_prefill_bwd")
+    unaligned(L.swattn_prefill_bwd(P, P, P, P, P, P, P, 100, P, 100, None, None, None, P, P, M,
+                                   1, 200, 200, 32, 8, 128, 64, 0.1, P, wsb, None),
+              "swattn_prefill_bwd")
+    unaligned(L.swattn_decode_fwd(P, P, M, P, P, P, P, 4, 100, 8, 2, 128, 64, 0.1, P, 1 << 30,
+                                  None), "swattn_decode_fwd")
+    unaligned(L.swattn_decode_fwd_noalloc(M, P, P, P, P, P, P, 4, 100, 8, 2, 128, 64, 0.1, None),
+              "swattn_decode_fwd_noalloc")
+    parts = (ctypes.c_void_p * 2)(P, M)
+    unaligned(L.swattn_merge_partials(parts, lses, 2, P, P, 10, 128, None),
+              "swattn_merge_partials")
+    parts = (ctypes.c_void_p * 2)(P, P)
+    unaligned(L.swattn_merge_partials(parts, lses, 2, M, P, 10, 128, None),
+              "swattn_merge_partials")
     print("host checks ok")
 ''')
 
