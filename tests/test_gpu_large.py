@@ -9,7 +9,8 @@ are checked against the oracle, which runs on just those rows: a sub-problem
 of the sampled query rows with their original key bounds passed as position
 metadata (full rows [0, p], local rows [p - W + 1, p], F:145-155) over the
 full K and V.  Bars as elsewhere: O max-abs <= 2e-2, mean-abs <= 2e-3, LSE
-relative <= 1e-3; dq relative L2 <= 1e-2, relative max <= 3e-2.
+relative <= 1e-3; dq, and dK / dV of the last 64 keys, relative L2 <= 1e-2,
+relative max <= 3e-2.
 """
 
 import numpy as np
@@ -78,6 +79,28 @@ def test_tensors_past_2gib_sampled_rows():
     mx = float(e.abs().max() / rq[0].abs().max())
     print(f"[large] dq sampled rows: rel_l2 {l2:.2e} rel_max {mx:.2e}", flush=True)
     assert l2 <= 1e-2 and mx <= 3e-2
+
+    # dK / dV of the last `late` keys: only rows at the last `late` positions
+    # see them (causal, and W > late), so those rows as a stand-alone problem
+    # over the full K / V give these keys' gradients exactly.  The dK/dV
+    # kernel gathers those Q / dO rows from byte offsets near 2^32.
+    late = 64
+    pl = np.arange(S - late, S)
+    assert mask_np[pl].any() and (~mask_np[pl]).any()
+    fi, li, md = _sub_problem(mask_np, pl)
+    sel = torch.as_tensor(pl, device=DEV)
+    _, rk, rv = oracle.routed_attention_backward(q[0, sel].unsqueeze(0).cpu(), kc, vc,
+                                                 do[0, sel].unsqueeze(0).cpu(), fi, li,
+                                                 window_size=W, metadata=md, chunk=8)
+    for name, got, ref in (("dk", dk, rk), ("dv", dv, rv)):
+        g_ = got[0, S - late:].float().cpu()
+        r_ = ref[0, S - late:]
+        e = g_ - r_
+        l2 = float(e.norm() / r_.norm())
+        mx = float(e.abs().max() / r_.abs().max())
+        print(f"[large] {name} of the last {late} keys: rel_l2 {l2:.2e} rel_max {mx:.2e}",
+              flush=True)
+        assert l2 <= 1e-2 and mx <= 3e-2
 
 
 def test_decode_caches_past_2gib():
