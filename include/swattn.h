@@ -255,8 +255,10 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *   dk, dv     bf16 like k: every key row is written (0 where no row sees it).
  *   workspace  >= swattn_prefill_bwd_workspace_bytes(...): 1 KiB of row
  *              info per KV head and 32 listed rows, plus a little (Q and dO
- *              are read in place, never copied); overwritten (calls sharing
- *              it must not overlap).
+ *              are read in place, never copied); for fewer than 512
+ *              (256-key tile, KV head) pairs also fp32 dK/dV partials of
+ *              256 KiB per split workgroup, at most 256 MiB in all;
+ *              overwritten (calls sharing it must not overlap).
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
  * ascending positions): the keys a row block can see are found by binary

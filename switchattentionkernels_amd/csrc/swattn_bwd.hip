@@ -43,10 +43,15 @@
 // * Keys outside a row's range get S = -inf, so P = 0 exactly; a row with no
 //   legal key (or a padding row) carries LSE = Delta = 0 and bounds [0, 0),
 //   is masked everywhere and contributes nothing.
+// * Grids of fewer than 512 (key tile, KV head) pairs split each pair over
+//   its row blocks (up to 16 workgroups); bwd_dkdv_reduce_kernel sums the
+//   fp32 partials in split order.  Pairs run longest first (the first key
+//   tiles of each sequence are seen by the most rows).
 // * dQ is a separate pass (S and dP recomputed) rather than atomics from the
 //   key-stationary pass, so every output is written once, deterministically.
 
 #include <limits.h>
+#include <algorithm>
 #include <math.h>
 
 #include "tiles.h"
@@ -75,6 +80,15 @@ constexpr int kOffQ = 0, kOffDO = kBlockBytes;
 constexpr int kRingSlots = 3;
 constexpr int kInfoSlots = 4;
 constexpr int kDkvLdsBytes = kVTileBytes + kRingSlots * kStageBytes + kInfoSlots * kInfoBytes;
+// dK/dV split partials: per workgroup and wave, 32 float4 units per lane (16
+// of dK^T, 16 of dV^T), unit-major so that a wave's store of one unit is
+// 1 KiB contiguous.
+constexpr int kPartUnits = 32;
+constexpr size_t kPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kPartUnits * 64 * 16;   // 256 KiB
+// Below this many dK/dV workgroups (two per CU on a 256-CU MI355X) the
+// (key tile, KV head) pairs are split over their row blocks.
+constexpr int64_t kDkvTargetWgs = 512;
+constexpr int kDkvMaxSplit = 16;
 // dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
 constexpr int kQStageBytes = 2 * kTileBytes;
 
@@ -99,6 +113,9 @@ struct BwdParams {
   char* info;                // [blocks][1 KiB]
   uint16_t* zero_row;        // 128 zeros: the gather source of rows that contribute nothing
   int32_t* ranges;           // [2][kv_tiles_dkv][2] block ranges
+  float* dkv_part;           // dK/dV split partials (dkv_split > 1): [workgroup][8 waves][32][64 lanes] float4
+  int32_t dkv_split;         // dK/dV workgroups per (key tile, KV head), over its row blocks
+  int32_t dkv_batches;       // > 1: key tiles ordered tile-in-sequence-major over this many sequences
   int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
@@ -337,6 +354,52 @@ __device__ __forceinline__ bf16x8 read_xt(const char* xb, int off0, int off1) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// (key tile, KV head) of dK/dV pair rank r.  Pairs run in rank order, KV
+// head fastest.  With dkv_batches > 1 (sequences of whole key tiles) tile i
+// of every sequence comes before tile i+1 of any: the first tiles of a causal
+// sequence are seen by the most rows, so the grid runs longest pairs first.
+__device__ __forceinline__ void dkv_pair(const BwdParams& p, int r, int& t, int& kvh) {
+  const int tr = r / p.hkv;
+  kvh = r - tr * p.hkv;
+  if (p.dkv_batches > 1) {
+    const int per_seq = p.kv_tiles_dkv / p.dkv_batches;
+    const int i = tr / p.dkv_batches;
+    t = (tr - i * p.dkv_batches) * per_seq + i;
+  } else {
+    t = tr;
+  }
+}
+
+// The bf16 dK / dV rows of one lane's key (lane half h) from its dK^T / dV^T
+// accumulators: element e of block d is d-row 32d + 8(e/4) + 4h + e%4.
+__device__ __forceinline__ void store_dkdv_rows(const BwdParams& p, int key, int kvh, int h,
+                                                const f32x16 (&dkt)[4], const f32x16 (&dvt)[4]) {
+  if (key >= p.total_kv) return;
+  const int64_t base = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 4 * h;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint2 uk, uv;
+      uk.x = pack_bf16x2(dkt[d][4 * j + 0] * p.scale, dkt[d][4 * j + 1] * p.scale);
+      uk.y = pack_bf16x2(dkt[d][4 * j + 2] * p.scale, dkt[d][4 * j + 3] * p.scale);
+      uv.x = pack_bf16x2(dvt[d][4 * j + 0], dvt[d][4 * j + 1]);
+      uv.y = pack_bf16x2(dvt[d][4 * j + 2], dvt[d][4 * j + 3]);
+      *reinterpret_cast<uint2*>(p.dk + base + 32 * d + 8 * j) = uk;
+      *reinterpret_cast<uint2*>(p.dv + base + 32 * d + 8 * j) = uv;
+    }
+  }
+}
+
+// Float4 unit u of (workgroup wg, wave, lane) in the split partials: units
+// 4d + j hold dK^T block d elements 4j .. 4j+3, units 16 + 4d + j the same of
+// dV^T.
+__device__ __forceinline__ float4* part_unit(const BwdParams& p, int64_t wg, int wave, int u,
+                                             int lane) {
+  return reinterpret_cast<float4*>(p.dkv_part) + ((wg * kBwdWaves + wave) * kPartUnits + u) * 64 +
+         lane;
+}
+
 __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
                           amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_kernel(const BwdParams p) {
   // [V tile: 256 key rows][three Q / dO block slots][four info slots]
@@ -346,7 +409,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   // stages, its source pointer) then stay scalar selects.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, h = lane >> 5;
-  const int t = blockIdx.x / p.hkv, kvh = blockIdx.x - (blockIdx.x / p.hkv) * p.hkv;
+  // Workgroup = (pair rank, split s): the rank gives the (key tile t, KV
+  // head) pair (dkv_pair); split s of dkv_split takes an equal share of the
+  // pair's row blocks (all of them without a split).
+  const int split = p.dkv_split;
+  const int pair = blockIdx.x / split;
+  const int s_idx = blockIdx.x - pair * split;
+  int t, kvh;
+  dkv_pair(p, pair, t, kvh);
   const int kw0 = t * kKeysDkv + 32 * wave;   // this wave's first key
   const int key = kw0 + n;                    // this lane's key (B column)
 
@@ -373,9 +443,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   const int b0lo = p.ranges[2 * t], b0hi = p.ranges[2 * t + 1];
   const int b1lo = p.ranges[2 * (nt + t)], b1hi = p.ranges[2 * (nt + t) + 1];
   const int n0 = max(b0hi - b0lo, 0), n1 = max(b1hi - b1lo, 0);
-  const int nb = n0 + n1;
+  const int chunk = (n0 + n1 + split - 1) / split;
+  const int first = min(n0 + n1, s_idx * chunk);
+  const int nb = min(n0 + n1 - first, chunk);   // this workgroup's blocks: first .. first+nb-1
   auto block_of = [&](int i) -> int64_t {
-    return i < n0 ? packed_block(p, 0, kvh, b0lo + i) : packed_block(p, 1, kvh, b1lo + i - n0);
+    const int a = first + i;
+    return a < n0 ? packed_block(p, 0, kvh, b0lo + a) : packed_block(p, 1, kvh, b1lo + a - n0);
   };
 
   const DkvPlan pl = make_dkv_plan(p, kvh, wave, lane);
@@ -498,23 +571,57 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     }
   }
 
-  // dK^T / dV^T element e of block d is d-row 32d + 8(e/4) + 4h + e%4 of key.
-  if (key < p.total_kv) {
-    const int64_t base = (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 4 * h;
+  if (split == 1) {
+    store_dkdv_rows(p, key, kvh, h, dkt, dvt);
+  } else {
+    // fp32 partials (zeros for a split with no blocks); bwd_dkdv_reduce_kernel
+    // sums the splits in order and stores the rows.
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint2 uk, uv;
-        uk.x = pack_bf16x2(dkt[d][4 * j + 0] * p.scale, dkt[d][4 * j + 1] * p.scale);
-        uk.y = pack_bf16x2(dkt[d][4 * j + 2] * p.scale, dkt[d][4 * j + 3] * p.scale);
-        uv.x = pack_bf16x2(dvt[d][4 * j + 0], dvt[d][4 * j + 1]);
-        uv.y = pack_bf16x2(dvt[d][4 * j + 2], dvt[d][4 * j + 3]);
-        *reinterpret_cast<uint2*>(p.dk + base + 32 * d + 8 * j) = uk;
-        *reinterpret_cast<uint2*>(p.dv + base + 32 * d + 8 * j) = uv;
+        *part_unit(p, blockIdx.x, wave, 4 * d + j, lane) =
+            make_float4(dkt[d][4 * j], dkt[d][4 * j + 1], dkt[d][4 * j + 2], dkt[d][4 * j + 3]);
+        *part_unit(p, blockIdx.x, wave, 16 + 4 * d + j, lane) =
+            make_float4(dvt[d][4 * j], dvt[d][4 * j + 1], dvt[d][4 * j + 2], dvt[d][4 * j + 3]);
       }
     }
   }
+}
+
+// dK / dV of split pairs: one thread per (pair, wave, float4 unit, lane).
+// It sums that unit over the splits in split order (deterministic) and stores
+// its four bf16 values where the unsplit kernel's epilogue would.
+static_assert(kPartUnits == 32 && kBwdWaves == 8, "the reduce's thread index splits 6 + 5 + 3 bits");
+__global__ __launch_bounds__(kThreads) void bwd_dkdv_reduce_kernel(const BwdParams p) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int lane = static_cast<int>(id & 63);
+  const int u = static_cast<int>((id >> 6) & (kPartUnits - 1));
+  const int wave = static_cast<int>((id >> 11) & (kBwdWaves - 1));
+  const int pair = static_cast<int>(id >> 14);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp = 0; sp < p.dkv_split; ++sp) {
+    const float4 a = *part_unit(p, static_cast<int64_t>(pair) * p.dkv_split + sp, wave, u, lane);
+    acc.x += a.x;
+    acc.y += a.y;
+    acc.z += a.z;
+    acc.w += a.w;
+  }
+  int t, kvh;
+  dkv_pair(p, pair, t, kvh);
+  const int key = t * kKeysDkv + 32 * wave + (lane & 31);
+  if (key >= p.total_kv) return;
+  // Unit 4d + j (+16 for dV): elements 4j .. 4j+3 of block d, i.e. d-rows
+  // 32d + 8j + 4h .. +3 of the key (lane half h).
+  const bool is_v = u >= 16;
+  const int d = (u & 15) >> 2, j = u & 3;
+  const float sc = is_v ? 1.0f : p.scale;
+  uint2 w;
+  w.x = pack_bf16x2(acc.x * sc, acc.y * sc);
+  w.y = pack_bf16x2(acc.z * sc, acc.w * sc);
+  uint16_t* dst = is_v ? p.dv : p.dk;
+  *reinterpret_cast<uint2*>(dst + (static_cast<int64_t>(key) * p.hkv + kvh) * kD + 4 * (lane >> 5) +
+                            32 * d + 8 * j) = w;
 }
 
 // ---------------------------------------------------------------------------
@@ -746,8 +853,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 // Host side.
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv;
-  size_t off_info, off_zero, off_ranges, bytes;
+  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv, dkv_split;
+  size_t off_info, off_zero, off_ranges, off_part, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -762,10 +869,18 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   }
   L.total_blocks = static_cast<int64_t>(heads_kv) * (L.blocks[0] + L.blocks[1]);
   L.kv_tiles_dkv = ceil_div(total_kv, kKeysDkv);
+  // Fewer (key tile, KV head) pairs than two rounds of workgroups: each pair
+  // is split over its row blocks, so that the longest pair (the first key
+  // tile sees every full row) no longer sets the kernel's length.
+  const int64_t pairs = L.kv_tiles_dkv * heads_kv;
+  L.dkv_split = pairs >= kDkvTargetWgs ? 1
+                : std::min<int64_t>(kDkvMaxSplit, ceil_div(kDkvTargetWgs, pairs));
   size_t o = 0;
   L.off_info = o;   o = align256(o + static_cast<size_t>(L.total_blocks) * kInfoBytes);
   L.off_zero = o;   o = align256(o + kRowBytes);
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
+  L.off_part = o;
+  if (L.dkv_split > 1) o += static_cast<size_t>(pairs * L.dkv_split) * kPartBytesPerWg;
   L.bytes = o;
   return L;
 }
@@ -875,6 +990,10 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.total_q = static_cast<int32_t>(total_q);
   p.total_kv = static_cast<int32_t>(total_kv);
   p.kv_tiles_dkv = static_cast<int32_t>(L.kv_tiles_dkv);
+  p.dkv_split = static_cast<int32_t>(L.dkv_split);
+  // Several sequences that each hold whole 256-key tiles: interleave them.
+  p.dkv_batches = (batch > 1 && seq_kv % kKeysDkv == 0) ? batch : 1;
+  p.dkv_part = reinterpret_cast<float*>(ws + L.off_part);
   p.hq = heads_q;
   p.hkv = heads_kv;
   p.group = static_cast<int32_t>(group);
@@ -897,8 +1016,13 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
       hipLaunchKernelGGL(bwd_prep_kernel<false>, dim3(static_cast<uint32_t>(nblk), heads_kv),
                          dim3(kThreads), 0, st, p);
   }
-  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(L.kv_tiles_dkv * heads_kv)),
+  const int64_t pairs = L.kv_tiles_dkv * heads_kv;
+  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(pairs * L.dkv_split)),
                      dim3(kBwdThreads), 0, st, p);
+  if (L.dkv_split > 1)
+    hipLaunchKernelGGL(bwd_dkdv_reduce_kernel,
+                       dim3(static_cast<uint32_t>(pairs * kBwdWaves * kPartUnits * 64 / kThreads)),
+                       dim3(kThreads), 0, st, p);
   const int64_t qgrid = (L.items[0] + L.items[1]) * heads_kv;
   if (qgrid > 0)
     hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(qgrid)), dim3(kBwdThreads), 0, st,

@@ -53,11 +53,17 @@ def test_version_and_workspace():
     assert lib.swattn_prefill_workspace_bytes(2, 100, 8, 128) == 8 * 4 * 16384
     assert lib.swattn_prefill_workspace_bytes(1, 100, 8, 64) == 0
     # backward: per KV head and 32-row block 1 KiB of row info (Q and dO are
-    # gathered in place, never copied), one 256-byte zero row, and 256-key
-    # block ranges (256-byte aligned).
+    # gathered in place, never copied), one 256-byte zero row, 256-key block
+    # ranges (256-byte aligned), and, with fewer than 512 (key tile, KV head)
+    # pairs, 256 KiB of fp32 dK/dV partials per split workgroup: here 4 key
+    # tiles x 8 KV heads = 32 pairs, split min(16, 512 / 32) = 16 ways.
     nb = 8 * (-(-(300 * 4) // 32) + -(-(700 * 4) // 32))
-    expect = nb * 1024 + 256 + 256
+    expect = nb * 1024 + 256 + 256 + 32 * 16 * 256 * 1024
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 128, 300, 700) == expect
+    # 512 or more pairs: no split, no partials
+    nb = 8 * (-(-(3000 * 4) // 32) + -(-(7000 * 4) // 32))
+    expect_big = nb * 1024 + 256 + 2 * 64 * 2 * 4     # 64 key tiles x 8 KV heads = 512 pairs
+    assert lib.swattn_prefill_bwd_workspace_bytes(1, 64 * 256, 32, 8, 128, 3000, 7000) == expect_big
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 30, 8, 128, 300, 700) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 64, 300, 700) == 0
 
