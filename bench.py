@@ -33,7 +33,9 @@ The JSON line also carries:
   the routed backward (dq, dk, dv) of the same prefill.
 
 ``--configs cpu,b2,s16k,varlen,s64k`` instead times the forward and the
-backward on each named workload (one JSON line each, no roofline).
+backward on each named workload (one JSON line each, no roofline);
+``--p-sweep 0,0.1,0.25,0.5,1`` times config #3's attention call at each
+router density, beside the dense-causal call (one JSON line each).
 """
 
 from __future__ import annotations
@@ -71,6 +73,9 @@ def parse():
     ap.add_argument("--decode-only", action="store_true",
                     help="only loop switch_gqa_decode_forward on the decode comparator's "
                          "workload (for rocprofv3 runs)")
+    ap.add_argument("--p-sweep", default="",
+                    help="comma-separated p_full values: config #3's attention call at each "
+                         "router density (e.g. 0,0.1,0.25,0.5,1)")
     ap.add_argument("--configs", default="",
                     help="comma-separated workloads (cpu,b2,s16k,varlen,s64k): time the "
                          "forward and the backward on each once the clock has settled, one "
@@ -146,6 +151,59 @@ def config_table(args):
             "bwd_ms": round(b_ms, 4), "bwd_tflops_2p5x": round(2.5 * flops / b_ms / 1e9, 1)}),
             flush=True)
         del q, k, v, m, o, lse, do, full, local, md
+        torch.cuda.empty_cache()
+
+
+def p_sweep(args):
+    """Config #3 (s16k) over router densities: the swattn_prefill_fwd call
+    (vt_pack_kernel + fwd_kernel) timed on its stream once the clock has
+    settled, its routed TFLOP/s and fraction of the bf16 MFMA peak, and its
+    time over the same call with every row routed full (dense causal) beside
+    the routed-FLOP fraction."""
+    from switchattentionkernels_amd import _lib, build_switch_query_indices, routed_flops, workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    dense_ms = None
+    for p in [float(x) for x in args.p_sweep.split(",")]:
+        wl = workloads.build("s16k", seed=args.seed, p_full=p)
+        d = wl["workload"]
+        B, S, HQ, HKV, W = d.batch, d.seq_len, d.heads_q, d.heads_kv, d.window
+        q, k, v, m = (wl[x].to(dev) for x in ("q", "k", "v", "mask"))
+        out = torch.empty_like(q)
+        lse = torch.empty(q.shape[:3], dtype=torch.float32, device=dev)
+        ws_bytes = int(L.swattn_prefill_workspace_bytes(B, S, HKV, 128))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        scale = 128 ** -0.5 * 1.4426950408889634
+
+        def attn(fi, li):
+            st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), fi.data_ptr(),
+                                      fi.numel(), li.data_ptr(), li.numel(), None, None, None,
+                                      out.data_ptr(), lse.data_ptr(), B, S, S, HQ, HKV, 128, W,
+                                      scale, ws.data_ptr(), ws_bytes, stream)
+            if st != 0:
+                raise RuntimeError(L.swattn_last_error().decode())
+
+        if dense_ms is None:
+            fa, la = build_switch_query_indices(torch.ones_like(m))
+            dense_ms = settled_ms(lambda: attn(fa, la))
+            dense_flops = routed_flops(fa, la, batch=B, seq_q=S, seq_kv=S, heads_q=HQ,
+                                       head_dim=128, window=W)
+        full, local = build_switch_query_indices(m)
+        flops = routed_flops(full, local, batch=B, seq_q=S, seq_kv=S, heads_q=HQ, head_dim=128,
+                             window=W)
+        ms = settled_ms(lambda: attn(full, local))
+        print(json.dumps({
+            "p_sweep": p, "workload": f"s16k: B{B} S{S} Hq{HQ}/Hkv{HKV} d128 W{W} Bernoulli "
+                                      f"p_full={p}, seed {args.seed}",
+            "full_rows": int(full.numel()), "routed_gflop": round(flops / 1e9, 2),
+            "entry_point_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
+            "frac_of_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "routed_flop_fraction": round(flops / dense_flops, 4),
+            "routed_over_dense_time": round(ms / dense_ms, 4), "dense_ms": round(dense_ms, 4)}),
+            flush=True)
+        del q, k, v, m, out, lse, ws, full, local
         torch.cuda.empty_cache()
 
 
@@ -227,6 +285,9 @@ def main():
 
     if args.configs:
         config_table(args)
+        return
+    if args.p_sweep:
+        p_sweep(args)
         return
 
     from switchattentionkernels_amd import (build_switch_query_indices, routed_flops,
