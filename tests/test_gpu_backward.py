@@ -94,6 +94,8 @@ def _md_np(md):
     (1, 384, 8, 2, 96, 1.0, None),      # all full (dense causal)
     (1, 300, 8, 2, 64, 0.4, 180),       # fewer keys than queries
     (2, 200, 8, 2, 50, 0.3, 333),       # more keys than queries
+    (3, 512, 8, 2, 100, 0.3, None),     # whole 256-key tiles per sequence: interleaved
+                                        # dK/dV pair order, 12 pairs split 16 ways
 ])
 def test_backward_matches_oracle(b, s, hq, hkv, w, p, skv):
     q, k, v, do = _qkv(b * 1000 + s, b, s, hq, hkv, skv)
