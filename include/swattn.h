@@ -257,8 +257,10 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *              info per KV head and 32 listed rows, plus a little (Q and dO
  *              are read in place, never copied); for fewer than 512
  *              (256-key tile, KV head) pairs also fp32 dK/dV partials of
- *              256 KiB per split workgroup, at most 256 MiB in all;
- *              overwritten (calls sharing it must not overlap).
+ *              256 KiB per split workgroup (at most 256 MiB), and for fewer
+ *              than 512 dQ workgroups fp32 dQ partials of 128 KiB per split
+ *              workgroup (at most 128 MiB); overwritten (calls sharing it
+ *              must not overlap).
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
  * ascending positions): the keys a row block can see are found by binary

@@ -46,7 +46,9 @@
 // * Grids of fewer than 512 (key tile, KV head) pairs split each pair over
 //   its row blocks (up to 16 workgroups); bwd_dkdv_reduce_kernel sums the
 //   fp32 partials in split order.  Pairs run longest first (the first key
-//   tiles of each sequence are seen by the most rows).
+//   tiles of each sequence are seen by the most rows).  dQ grids of fewer
+//   than 512 workgroups split each row tile over its key tiles the same
+//   way (bwd_dq_reduce_kernel).
 // * dQ is a separate pass (S and dP recomputed) rather than atomics from the
 //   key-stationary pass, so every output is written once, deterministically.
 
@@ -89,6 +91,11 @@ constexpr size_t kPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kPartUnits *
 // (key tile, KV head) pairs are split over their row blocks.
 constexpr int64_t kDkvTargetWgs = 512;
 constexpr int kDkvMaxSplit = 16;
+// dQ split partials: per workgroup and wave, 16 float4 units per lane (dQ^T
+// block d elements 4j .. 4j+3 in unit 4d + j), unit-major like the dK/dV ones.
+constexpr int kDqPartUnits = 16;
+constexpr size_t kDqPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kDqPartUnits * 64 * 16;   // 128 KiB
+constexpr int kDqMinTilesPerSplit = 4;   // 64-key tiles a dQ split takes at least
 // dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
 constexpr int kQStageBytes = 2 * kTileBytes;
 
@@ -116,6 +123,8 @@ struct BwdParams {
   float* dkv_part;           // dK/dV split partials (dkv_split > 1): [workgroup][8 waves][32][64 lanes] float4
   int32_t dkv_split;         // dK/dV workgroups per (key tile, KV head), over its row blocks
   int32_t dkv_batches;       // > 1: key tiles ordered tile-in-sequence-major over this many sequences
+  float* dq_part;            // dQ split partials (dq_split > 1): [workgroup][8 waves][16][64 lanes] float4
+  int32_t dq_split;          // dQ workgroups per (branch, row tile, KV head), over its key tiles
   int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
@@ -400,6 +409,14 @@ __device__ __forceinline__ float4* part_unit(const BwdParams& p, int64_t wg, int
          lane;
 }
 
+// Float4 unit u (= 4d + j: dQ^T block d elements 4j .. 4j+3) of (workgroup
+// wg, wave, lane) in the dQ split partials.
+__device__ __forceinline__ float4* dq_part_unit(const BwdParams& p, int64_t wg, int wave, int u,
+                                                int lane) {
+  return reinterpret_cast<float4*>(p.dq_part) + ((wg * kBwdWaves + wave) * kDqPartUnits + u) * 64 +
+         lane;
+}
+
 __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
                           amdgpu_waves_per_eu(2, 2))) void bwd_dkdv_kernel(const BwdParams p) {
   // [V tile: 256 key rows][three Q / dO block slots][four info slots]
@@ -673,8 +690,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   // stages, its source pointer) then stay scalar selects.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, h = lane >> 5;
+  // Workgroup = ((row tile t, split s), KV head), KV head fastest: split s
+  // of dq_split takes an equal share of the tile's key tiles.
   const int kvh = blockIdx.x % p.hkv;
-  const int t = blockIdx.x / p.hkv;
+  const int ts = blockIdx.x / p.hkv;
+  const int t = ts / p.dq_split;
+  const int s_idx = ts - t * p.dq_split;
   const int b = t < p.items[0] ? 0 : 1;
   // Latest positions first in each branch (longest rows first).
   const int item = b == 0 ? p.items[0] - 1 - t : p.items[0] + p.items[1] - 1 - t;
@@ -728,8 +749,12 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     g_s = min(g_s, s_range[i]);
     g_e = max(g_e, s_range[kBwdWaves + i]);
   }
-  const int t_begin = g_e > g_s ? g_s / kBN : 0;
-  const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
+  const int t_all0 = g_e > g_s ? g_s / kBN : 0;
+  const int t_all1 = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
+  // This split's key tiles [t_begin, t_end).
+  const int dq_chunk = (t_all1 - t_all0 + p.dq_split - 1) / p.dq_split;
+  const int t_begin = t_all0 + min(t_all1 - t_all0, s_idx * dq_chunk);
+  const int t_end = min(t_all1, t_begin + dq_chunk);
   // Tiles inside the range of every row this wave stores need no mask.  A
   // stored row with no key (start = end = 0) must see every tile masked, so
   // it counts as start = +inf, end = -inf; lanes that store nothing do not
@@ -831,6 +856,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
 
   const int G = p.group;
+  if (p.dq_split > 1) {
+    // fp32 partials (zeros for a split with no tiles); bwd_dq_reduce_kernel
+    // sums the splits in order and stores the rows.
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *dq_part_unit(p, blockIdx.x, wave, 4 * d + j, lane) =
+            make_float4(dqt[d][4 * j], dqt[d][4 * j + 1], dqt[d][4 * j + 2], dqt[d][4 * j + 3]);
+    }
+    return;
+  }
   const int q_slot = r / G;
   const int pos = valid ? p.idx[b][q_slot] : 0;
   if (valid && pos_ok(p, pos)) {
@@ -849,18 +886,57 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
 }
 
+// dQ of split row tiles: one thread per (row tile and KV head, wave, float4
+// unit, lane).  It sums that unit over the splits in split order
+// (deterministic) and stores its four bf16 values where the unsplit kernel
+// would: the lane's row of the tile, d-rows 32d + 8j + 4h .. +3.
+static_assert(kDqPartUnits == 16 && kBwdWaves == 8, "the reduce's thread index splits 6 + 4 + 3 bits");
+__global__ __launch_bounds__(kThreads) void bwd_dq_reduce_kernel(const BwdParams p) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  const int lane = static_cast<int>(id & 63);
+  const int u = static_cast<int>((id >> 6) & (kDqPartUnits - 1));
+  const int wave = static_cast<int>((id >> 10) & (kBwdWaves - 1));
+  const int tk = static_cast<int>(id >> 13);   // (row tile t, KV head), KV head fastest
+  const int kvh = tk % p.hkv, t = tk / p.hkv;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp = 0; sp < p.dq_split; ++sp) {
+    const int64_t wg = (static_cast<int64_t>(t) * p.dq_split + sp) * p.hkv + kvh;
+    const float4 a = *dq_part_unit(p, wg, wave, u, lane);
+    acc.x += a.x;
+    acc.y += a.y;
+    acc.z += a.z;
+    acc.w += a.w;
+  }
+  const int b = t < p.items[0] ? 0 : 1;
+  const int item = b == 0 ? p.items[0] - 1 - t : p.items[0] + p.items[1] - 1 - t;
+  const int blk = item * (kRowsPerItem / kBRows) + wave;
+  const int r = blk * kBRows + (lane & 31);
+  if (blk >= p.blocks[b] || r >= p.nrows[b]) return;
+  const int G = p.group;
+  const int q_slot = r / G;
+  const int pos = p.idx[b][q_slot];
+  if (!pos_ok(p, pos)) return;
+  const int qh = kvh * G + (r - q_slot * G);
+  const int d = u >> 2, j = u & 3;
+  uint2 w;
+  w.x = pack_bf16x2(acc.x * p.scale, acc.y * p.scale);
+  w.y = pack_bf16x2(acc.z * p.scale, acc.w * p.scale);
+  *reinterpret_cast<uint2*>(p.dq + (static_cast<int64_t>(pos) * p.hq + qh) * kD +
+                            4 * (lane >> 5) + 32 * d + 8 * j) = w;
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv, dkv_split;
-  size_t off_info, off_zero, off_ranges, off_part, bytes;
+  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv, dkv_split, dq_split;
+  size_t off_info, off_zero, off_ranges, off_part, off_dq_part, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, int64_t n_full,
-                            int64_t n_local) {
+inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, int64_t group,
+                            int64_t n_full, int64_t n_local) {
   BwdLayout L{};
   const int64_t n[2] = {n_full, n_local};
   for (int b = 0; b < 2; ++b) {
@@ -881,6 +957,18 @@ inline BwdLayout bwd_layout(int64_t total_kv, int32_t heads_kv, int64_t group, i
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.off_part = o;
   if (L.dkv_split > 1) o += static_cast<size_t>(pairs * L.dkv_split) * kPartBytesPerWg;
+  // dQ likewise: fewer row tiles (times KV heads) than two rounds of
+  // workgroups, each split over its key tiles, at least
+  // kDqMinTilesPerSplit of the longest possible range (one sequence's keys)
+  // per split.
+  const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
+  const int64_t max_tiles = ceil_div(seq_kv, kBN) + 1;
+  L.dq_split = 1;
+  if (q_items > 0 && q_items < kDkvTargetWgs)
+    L.dq_split = std::max<int64_t>(1, std::min<int64_t>({kDkvMaxSplit, ceil_div(kDkvTargetWgs, q_items),
+                                                         max_tiles / kDqMinTilesPerSplit}));
+  L.off_dq_part = o;
+  if (L.dq_split > 1) o += static_cast<size_t>(q_items * L.dq_split) * kDqPartBytesPerWg;
   L.bytes = o;
   return L;
 }
@@ -898,7 +986,7 @@ extern "C" size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_
   if (batch < 1 || seq_kv < 1 || heads_q < 1 || heads_kv < 1 || head_dim != kD ||
       heads_q % heads_kv != 0 || n_full < 0 || n_local < 0)
     return 0;
-  const BwdLayout L = bwd_layout(static_cast<int64_t>(batch) * seq_kv, heads_kv,
+  const BwdLayout L = bwd_layout(seq_kv, static_cast<int64_t>(batch) * seq_kv, heads_kv,
                                  heads_q / heads_kv, n_full, n_local);
   return L.bytes;
 }
@@ -948,7 +1036,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
       (n_full + n_local > 0 &&
        (!aligned16(q) || !aligned16(out) || !aligned16(dout) || !aligned16(dq))))
     return invalid("swattn_prefill_bwd: q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
-  const BwdLayout L = bwd_layout(total_kv, heads_kv, group, n_full, n_local);
+  const BwdLayout L = bwd_layout(seq_kv, total_kv, heads_kv, group, n_full, n_local);
   if (workspace == nullptr || workspace_bytes < L.bytes) {
     set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
     return SWATTN_EWORKSPACE;
@@ -994,6 +1082,8 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   // Several sequences that each hold whole 256-key tiles: interleave them.
   p.dkv_batches = (batch > 1 && seq_kv % kKeysDkv == 0) ? batch : 1;
   p.dkv_part = reinterpret_cast<float*>(ws + L.off_part);
+  p.dq_split = static_cast<int32_t>(L.dq_split);
+  p.dq_part = reinterpret_cast<float*>(ws + L.off_dq_part);
   p.hq = heads_q;
   p.hkv = heads_kv;
   p.group = static_cast<int32_t>(group);
@@ -1023,9 +1113,14 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
     hipLaunchKernelGGL(bwd_dkdv_reduce_kernel,
                        dim3(static_cast<uint32_t>(pairs * kBwdWaves * kPartUnits * 64 / kThreads)),
                        dim3(kThreads), 0, st, p);
-  const int64_t qgrid = (L.items[0] + L.items[1]) * heads_kv;
-  if (qgrid > 0)
-    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(qgrid)), dim3(kBwdThreads), 0, st,
-                       p);
+  const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
+  if (q_items > 0) {
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(q_items * L.dq_split)),
+                       dim3(kBwdThreads), 0, st, p);
+    if (L.dq_split > 1)
+      hipLaunchKernelGGL(bwd_dq_reduce_kernel,
+                         dim3(static_cast<uint32_t>(q_items * kBwdWaves * kDqPartUnits * 64 / kThreads)),
+                         dim3(kThreads), 0, st, p);
+  }
   return launch_status("swattn_prefill_bwd");
 }

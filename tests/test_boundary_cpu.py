@@ -56,9 +56,11 @@ def test_version_and_workspace():
     # gathered in place, never copied), one 256-byte zero row, 256-key block
     # ranges (256-byte aligned), and, with fewer than 512 (key tile, KV head)
     # pairs, 256 KiB of fp32 dK/dV partials per split workgroup: here 4 key
-    # tiles x 8 KV heads = 32 pairs, split min(16, 512 / 32) = 16 ways.
+    # tiles x 8 KV heads = 32 pairs, split min(16, 512 / 32) = 16 ways.  dQ:
+    # (5 + 11 row tiles of 256) x 8 KV heads = 128 items, split min(16,
+    # 512 / 128, (ceil(1000 / 64) + 1) // 4) = 4 ways, 128 KiB each.
     nb = 8 * (-(-(300 * 4) // 32) + -(-(700 * 4) // 32))
-    expect = nb * 1024 + 256 + 256 + 32 * 16 * 256 * 1024
+    expect = nb * 1024 + 256 + 256 + 32 * 16 * 256 * 1024 + 128 * 4 * 128 * 1024
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 128, 300, 700) == expect
     # 512 or more pairs: no split, no partials
     nb = 8 * (-(-(3000 * 4) // 32) + -(-(7000 * 4) // 32))
