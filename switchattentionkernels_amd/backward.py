@@ -33,13 +33,15 @@ def _check_monotone(metadata: SwitchAttentionMetadata, full: torch.Tensor,
                     local: torch.Tensor) -> None:
     """The backward finds the rows that see a key block by binary search, so
     each list's key bounds must be non-decreasing along the list (true for
-    every single causal sequence and for packed sequences in order).  One
-    device-to-host read."""
+    every single causal sequence and for packed sequences in order).  A
+    start past its row's end is an empty range and counts as the end, as in
+    the kernels.  One device-to-host read."""
     ok = torch.ones((), dtype=torch.bool, device=full.device)
     for lst, starts in ((full, metadata.full_starts), (local, metadata.local_starts)):
         if lst.numel() > 1:
             li = lst.long()
-            for b in (starts[li], metadata.causal_ends[li]):
+            ends = metadata.causal_ends[li]
+            for b in (torch.minimum(starts[li], ends), ends):
                 ok = ok & (b[1:] >= b[:-1]).all()
     if not bool(ok.item()):
         raise ValueError(MSG_META + ": key bounds must be non-decreasing along each index list "

@@ -153,6 +153,11 @@ __device__ __forceinline__ void row_bounds(const BwdParams& p, int branch, int p
   }
   ks = max(ks, 0);
   ke = min(ke, p.total_kv);
+  // An empty range keeps ks = ke.  F's rule with seq_q > seq_kv + window - 1
+  // gives late local rows a start past their end (and past the next
+  // sequence's first start); clipped, the starts are non-decreasing along
+  // each list, as bwd_ranges_kernel's binary search needs.
+  ks = min(ks, ke);
 }
 
 __device__ __forceinline__ int64_t packed_block(const BwdParams& p, int b, int kvh, int blk) {

@@ -96,6 +96,9 @@ def _md_np(md):
     (2, 200, 8, 2, 50, 0.3, 333),       # more keys than queries
     (3, 512, 8, 2, 100, 0.3, None),     # whole 256-key tiles per sequence: interleaved
                                         # dK/dV pair order, 12 pairs split 16 ways
+    (3, 164, 8, 1, 2, 0.3, 3),          # seq_q > seq_kv + W - 1: late local rows have
+    (2, 300, 8, 2, 64, 0.3, 100),       # empty ranges starting past the next sequence's
+                                        # first start (the block search must still find it)
 ])
 def test_backward_matches_oracle(b, s, hq, hkv, w, p, skv):
     q, k, v, do = _qkv(b * 1000 + s, b, s, hq, hkv, skv)
