@@ -102,8 +102,12 @@ def routed_attention(q, k, v, full_idx, local_idx, *, window_size=1024,
         o = torch.bmm(p.reshape(hkv, len(r) * g, ke - ks),
                       vf[ks:ke].permute(1, 0, 2).contiguous())              # [Hkv, R*G, D]
         o = o.reshape(hkv, len(r), g, d).permute(1, 0, 2, 3).reshape(len(r), hq, d)
+        lse_r = (lse_nat * LOG2E).permute(1, 0, 2).reshape(len(r), hq)
+        # A row with no legal key is 0 / 0 = NaN (V:236-241), also when every
+        # row of the chunk is empty and the contraction over no key gives 0.
+        o = o.masked_fill(torch.isneginf(lse_r)[..., None], float("nan"))
         out[torch.from_numpy(r)] = o
-        lse[torch.from_numpy(r)] = (lse_nat * LOG2E).permute(1, 0, 2).reshape(len(r), hq)
+        lse[torch.from_numpy(r)] = lse_r
     return out.reshape(batch, seq_q, hq, d), lse.reshape(batch, seq_q, hq)
 
 

@@ -274,6 +274,21 @@ def test_empty_row_is_nan_like_the_reference():
     assert lse[0, 2, 0] == float("-inf")
 
 
+def test_empty_rows_are_nan_in_any_chunk():
+    """Rows with no legal key are NaN / -inf whether or not other rows of the
+    oracle's chunk have keys: with 10 keys and W = 3, local rows from 12 on
+    see none (their start passes the last key), and with chunk = 4 the chunks
+    [12, 16) and [16, 20) hold only such rows."""
+    q, k, v = _rand_qkv(23, 1, 20, 2, 1, skv=10)
+    full, local = R.compact(np.zeros((1, 20), dtype=bool))
+    o, lse = oracle.routed_attention(q, k, v, full, local, window_size=3, chunk=4)
+    assert torch.isnan(o[0, 12:]).all() and torch.isneginf(lse[0, 12:]).all()
+    assert torch.isfinite(o[0, :12]).all() and torch.isfinite(lse[0, :12]).all()
+    # the same rows inside mixed chunks agree
+    o8, lse8 = oracle.routed_attention(q, k, v, full, local, window_size=3, chunk=8)
+    assert torch.equal(torch.isnan(o8), torch.isnan(o))
+
+
 def test_routed_flops_equals_pair_count():
     m = _mask(20, (2, 77), 0.3)
     full, local = R.compact(m.numpy())
