@@ -72,6 +72,9 @@ def _assert_close(o, lse, o_ref, lse_ref, rows=None, tag=""):
     o, o_ref = o[~empty], o_ref[~empty]
     fin = torch.isfinite(lse_ref)
     lse, lse_ref = lse[fin], lse_ref[fin]
+    if o.numel() == 0:   # every row empty: the NaN / -inf patterns above are the whole check
+        print(f"{tag}: every row empty (NaN / -inf patterns match)", flush=True)
+        return
     err = (o - o_ref).abs()
     mx, mean = err.max().item(), err.mean().item()
     lerr = ((lse - lse_ref).abs() / lse_ref.abs().clamp(min=1.0)).max().item()
