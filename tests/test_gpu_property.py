@@ -59,7 +59,7 @@ def _case(c):
     return q, k, v, mask, gen, tag
 
 
-@settings(max_examples=40, **SETTINGS)
+@settings(max_examples=80, **SETTINGS)
 @given(c=shapes)
 def test_forward_property(c):
     q, k, v, mask, _, tag = _case(c)
@@ -82,7 +82,7 @@ def _grad_close(got, ref, tag):
     assert l2 <= 1e-2 and mx <= 3e-2, f"{tag}: rel_l2 {l2:.3e} rel_max {mx:.3e}"
 
 
-@settings(max_examples=20, **SETTINGS)
+@settings(max_examples=40, **SETTINGS)
 @given(c=shapes)
 def test_backward_property(c):
     q, k, v, mask, gen, tag = _case(c)
@@ -128,7 +128,7 @@ def test_logits_compaction_property(b, s, dtype, thr, special, seed):
     assert torch.equal(f, f_ref) and torch.equal(l, l_ref), (b, s, dtype, thr, seed)
 
 
-@settings(max_examples=40, **SETTINGS)
+@settings(max_examples=60, **SETTINGS)
 @given(c=st.fixed_dictionaries({
     "b": st.integers(1, 40),
     "cache": st.integers(1, 3000),
@@ -161,7 +161,7 @@ def test_decode_property(c):
     _assert_close(o.unsqueeze(1), lse.unsqueeze(1), o_r.unsqueeze(1), lse_r.unsqueeze(1), tag=tag)
 
 
-@settings(max_examples=20, **SETTINGS)
+@settings(max_examples=40, **SETTINGS)
 @given(c=st.fixed_dictionaries({
     "s": st.integers(2, 600),
     "hkv": st.integers(1, 2),
@@ -193,7 +193,7 @@ def test_split_merge_property(c):
     _assert_close(o, lse, o_r, lse_r, tag=tag)
 
 
-@settings(max_examples=20, **SETTINGS)
+@settings(max_examples=40, **SETTINGS)
 @given(c=st.fixed_dictionaries({
     "lens": st.lists(st.integers(1, 250), min_size=1, max_size=5),
     "hkv": st.integers(1, 2),
