@@ -528,17 +528,19 @@ def test_shard_bounds_bit_exact():
         assert np.array_equal(md.causal_ends.cpu().numpy(), e)
 
 
-def test_merge_kernel_matches_oracle():
-    gen = torch.Generator().manual_seed(12)
+@pytest.mark.parametrize("n_parts", [1, 3, 16])   # 16: the most one call merges
+def test_merge_kernel_matches_oracle(n_parts):
+    gen = torch.Generator().manual_seed(12 + n_parts)
     shape = (1, 300, 6)
     outs, lses = [], []
-    for i in range(3):
+    for i in range(n_parts):
         outs.append((torch.randn(*shape, 128, generator=gen) * 2).to(torch.bfloat16))
         l = torch.randn(*shape, generator=gen) * 20
         l[torch.rand(*shape, generator=gen) < 0.2] = -math.inf     # parts with no key
         lses.append(l)
-    lses[0][0, :5] = lses[1][0, :5] = lses[2][0, :5] = -math.inf   # rows empty everywhere
-    for i in range(3):   # an empty part's O is NaN, as the forward writes it
+    for i in range(n_parts):
+        lses[i][0, :5] = -math.inf                                  # rows empty everywhere
+    for i in range(n_parts):   # an empty part's O is NaN, as the forward writes it
         outs[i][torch.isneginf(lses[i])] = float("nan")
     o, l = merge_attention_partials([x.to(DEV) for x in outs], [x.to(DEV) for x in lses])
     o_r, l_r = oracle.merge_partials([x.float() for x in outs], lses)
