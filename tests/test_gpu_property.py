@@ -1,7 +1,8 @@
 """Property-based sweeps over small shapes (hypothesis): the HIP forward, the
 HIP backward, packed sequences (forward and backward), the compaction (from
-a mask and from router logits), the routed decode and split-then-merged key
-ranges against the CPU oracle.
+a mask and from router logits), the routed decode, split-then-merged key
+ranges, the forward on arbitrary caller key bounds and the backward on
+monotone caller key bounds, against the CPU oracle.
 
 The examples are derandomized: every run draws the same fixed set of shapes
 (batch, lengths, head counts, group size, window, routing density, key
@@ -232,3 +233,88 @@ def test_varlen_property(c):
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")
 
+
+
+def _metadata(fs, ls, ce, s, skv):
+    """Caller-made position metadata for one sequence of s queries over skv keys."""
+    from switchattentionkernels_amd.metadata import SwitchAttentionMetadata
+    i32 = lambda a: torch.as_tensor(np.asarray(a, dtype=np.int32), device=DEV)
+    return SwitchAttentionMetadata(i32(np.arange(s)), i32(np.arange(skv)), i32(np.zeros(s)),
+                                   i32(np.zeros(skv)), i32(fs), i32(ls), i32(ce))
+
+
+bounds_case = st.fixed_dictionaries({
+    "s": st.integers(1, 500),
+    "skv": st.integers(1, 600),
+    "hkv": st.integers(1, 2),
+    "g": st.sampled_from([1, 4, 5, 8]),
+    "p": st.sampled_from([0.0, 0.3, 1.0]),
+    "seed": st.integers(0, 2 ** 16),
+})
+
+
+@settings(max_examples=40, **SETTINGS)
+@given(c=bounds_case)
+def test_forward_arbitrary_bounds_property(c):
+    """Caller metadata may hold any key bounds (the reference validates only
+    their shapes, V:360-383): half the rows get a sensible [start, end), the
+    others random values from below 0 to past the last key, inverted or not,
+    in no order.  Bounds are clipped to [0, keys); an empty or inverted range
+    is an empty row (NaN / -inf), as in the oracle."""
+    s, skv, hkv = c["s"], c["skv"], c["hkv"]
+    hq = c["g"] * hkv
+    rng = np.random.default_rng(c["seed"])
+    gen = torch.Generator().manual_seed(c["seed"])
+    q, k, v = workloads.make_qkv(gen, 1, s, skv, hq, hkv, 128)
+    mask = torch.rand((1, s), generator=gen) < c["p"]
+    ce = rng.integers(-20, skv + 20, s)
+    fs, ls = rng.integers(-20, skv + 20, s), rng.integers(-20, skv + 20, s)
+    sane = rng.random(s) < 0.5
+    lo = rng.integers(0, skv, s)
+    hi = np.minimum(lo + rng.integers(1, skv + 1, s), skv)
+    fs, ce = np.where(sane, lo, fs), np.where(sane, hi, ce)
+    ls = np.where(sane, np.maximum(lo, hi - rng.integers(1, 300, s)), ls)
+    tag = f"bounds s{s} skv{skv} {hq}/{hkv} p{c['p']} seed{c['seed']}"
+    print(f"[property] {tag}", flush=True)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
+                                        metadata=_metadata(fs, ls, ce, s, skv))
+    torch.cuda.synchronize()
+    f_np, l_np = R.compact(mask.numpy())
+    o_ref, lse_ref = oracle.routed_attention(
+        q, k, v, f_np, l_np, metadata={"full_starts": fs, "local_starts": ls, "causal_ends": ce})
+    _assert_close(o, lse, o_ref, lse_ref, tag=tag)
+
+
+@settings(max_examples=20, **SETTINGS)
+@given(c=bounds_case)
+def test_backward_monotone_bounds_property(c):
+    """The backward takes any caller metadata whose key bounds do not
+    decrease along each list (starts past their end count as the end):
+    random sorted bounds, some rows empty, against the oracle."""
+    s, skv, hkv = c["s"], c["skv"], c["hkv"]
+    hq = c["g"] * hkv
+    rng = np.random.default_rng(c["seed"])
+    gen = torch.Generator().manual_seed(c["seed"])
+    q, k, v = workloads.make_qkv(gen, 1, s, skv, hq, hkv, 128)
+    mask = torch.rand((1, s), generator=gen) < c["p"]
+    do = torch.randn(q.shape, generator=gen).to(torch.bfloat16)
+    ce = np.sort(rng.integers(-5, skv + 5, s))
+    fs = np.maximum.accumulate(np.minimum(np.sort(rng.integers(-5, skv + 5, s)),
+                                          ce + rng.integers(0, 3, s)))
+    ls = np.maximum.accumulate(np.minimum(np.sort(rng.integers(-5, skv + 5, s)),
+                                          ce + rng.integers(0, 3, s)))
+    tag = f"monotone bounds s{s} skv{skv} {hq}/{hkv} p{c['p']} seed{c['seed']}"
+    print(f"[property] {tag}", flush=True)
+    md = _metadata(fs, ls, ce, s, skv)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_forward(qd, kd, vd, full, local, metadata=md)
+    grads = switch_gqa_prefill_backward(qd, kd, vd, o, lse, do.to(DEV), full, local, metadata=md)
+    torch.cuda.synchronize()
+    f_np, l_np = R.compact(mask.numpy())
+    refs = oracle.routed_attention_backward(
+        q, k, v, do, f_np, l_np,
+        metadata={"full_starts": fs, "local_starts": ls, "causal_ends": ce})
+    for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
+        _grad_close(g, r, f"{tag} {name}")
