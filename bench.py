@@ -557,7 +557,7 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false>",
+                     "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false, false>",
                      "kernel_ms": round(attn_ms, 4),
                      "kernel_timing": f"HIP events on the launch stream around "
                                       f"{max(args.steps, 50)} back-to-back calls after 10 "

@@ -126,6 +126,24 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
                                       int32_t head_dim);
 
 /*
+ * Workspace bytes that let swattn_prefill_fwd split long full-attention items
+ * by key range; no counterpart in the reference, whose grid is one CTA per
+ * query tile and head (V:402-445).  When the longest full item (a causal row
+ * tile late in a sequence) is long against the rest of the work, as with few
+ * KV heads (one GPU's share of a KV-head split), a workgroup per 2048-key
+ * chunk and a merge of the chunks by their log2 LSE (V:236-241) keep it from
+ * setting the kernel's length.  Returns swattn_prefill_workspace_bytes() when
+ * no split would run, a larger size (fp32 partial rows of the split items)
+ * when it would, 0 for an unsupported shape.  The forward splits only if it
+ * receives at least this much workspace; with less it runs unsplit.  Rows of
+ * items that lie inside one chunk are computed exactly as without a split.
+ */
+size_t swattn_prefill_split_workspace_bytes(int32_t batch, int64_t seq_q, int64_t seq_kv,
+                                            int32_t heads_q, int32_t heads_kv,
+                                            int32_t head_dim, int32_t window, int64_t n_full,
+                                            int64_t n_local);
+
+/*
  * Routed GQA prefill forward, both branches in one launch.  Replaces the two
  * _switch_gqa_prefill_branch launches of switch_gqa_prefill_forward
  * (V:402-445; kernel body V:103-249, fixed-length rule F:69-214).
@@ -143,8 +161,10 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
  *        lse uses the log2 convention: log2(sum_j 2^(s_j*c)) with
  *        c = scale_log2 and s_j the raw q.k products (V:236-241).
  *   scale_log2  softmax scale already multiplied by log2(e) (V:73-76).
- *   workspace   device scratch of at least swattn_prefill_workspace_bytes();
- *               overwritten by the call (calls sharing it must not overlap).
+ *   workspace   device scratch of at least swattn_prefill_workspace_bytes()
+ *               (swattn_prefill_split_workspace_bytes() to allow the key-range
+ *               split); overwritten by the call (calls sharing it must not
+ *               overlap).
  */
 int swattn_prefill_fwd(const void* q, const void* k, const void* v,
                        const int32_t* full_idx, int64_t n_full,

@@ -25,6 +25,8 @@ SIGNATURES = {
     "swattn_build_metadata": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _i32,
                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "swattn_prefill_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32]),
+    "swattn_prefill_split_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i64, _i32, _i32,
+                                                               _i32, _i32, _i64, _i64]),
     "swattn_decode_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32]),
     "swattn_decode_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i32,
                                          _i32, _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t,

@@ -57,9 +57,18 @@
 //   an exact running max.
 // * Tiles outside a wave's key range are skipped and interior tiles skip the
 //   mask.
+// * Key-range split (fwd_kernel<., true>, host plan in split_plan): when the
+//   longest causal item is long against the rest of the work (few KV heads,
+//   e.g. one GPU's share of a KV-head split), each full item runs as one
+//   workgroup per 2048-key chunk of its range.  The chunks' fp32 O rows and
+//   LSE go to the workspace and fwd_merge_kernel folds them (log2 LSE,
+//   V:236-241).  Chunk boundaries are fixed multiples of 2048 keys, and an
+//   item inside one chunk is computed exactly as without a split.
 
 #include <limits.h>
 #include <math.h>
+
+#include <algorithm>
 
 #include "tiles.h"
 
@@ -103,7 +112,18 @@ struct FwdParams {
   int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
+  // Key-range split of full items (maxc > 1): a full item whose key tiles
+  // cross a multiple of kSplitTiles runs as one workgroup per such chunk.
+  int32_t maxc;              // chunk slots per full item (1: no split)
+  float* part_o;             // [full item][slot][128 rows][128] fp32 O of the chunk (normalised)
+  float* part_lse;           // [full item][slot][128 rows] log2 LSE of the chunk (-inf: no key)
+  int2* part_n;              // [full item] (chunks, first chunk); chunks > 1: merge needed
 };
+
+// Chunk of the key-range split, in 64-key tiles (2048 keys).  Boundaries sit
+// at fixed multiples of it, so a row's chunks depend only on its own range,
+// and an item inside one chunk is computed exactly as without a split.
+constexpr int kSplitTiles = 32;
 
 // Per-lane staging plan for one 64-key tile (constant across tiles): K rows
 // and V^T rows go 1 KiB (one lane-linear load) at a time; each wave stages
@@ -423,7 +443,9 @@ __device__ __forceinline__ void pipe_step(const FwdParams& p, const StagePlan& s
     pipe_body<kPar, false, false>(smem, sp, krs, vrs, j, w, sb);
 }
 
-template <bool kMeta>
+// kSplit: the grid holds p.maxc chunk slots per full item (key-range split);
+// without it, the kernel has none of the split's code.
+template <bool kMeta, bool kSplit>
 __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
                           amdgpu_waves_per_eu(2, 2))) void fwd_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kSmemBytes];
@@ -433,10 +455,14 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   const int lane = tid & 63, wave = tid >> 6;
   const int rl = lane & 31, hh = lane >> 5;
 
-  // ---- work item -> (branch, tile, kv head) --------------------------------
+  // ---- work item -> (branch, tile, chunk slot, kv head) ----------------------
+  // Full tiles come first, each as maxc chunk slots in a row; KV head fastest.
   const int item = blockIdx.x;
   const int kvh = item % p.hkv;
-  const int t = item / p.hkv;
+  const int tq = item / p.hkv;
+  const int full_slots = kSplit ? p.tiles[0] * p.maxc : p.tiles[0];
+  const int t = !kSplit ? tq : tq < full_slots ? tq / p.maxc : p.tiles[0] + (tq - full_slots);
+  const int cslot = kSplit && tq < full_slots ? tq - t * p.maxc : 0;
   const int branch = t < p.tiles[0] ? 0 : 1;
   // Both branches run their last tile (latest positions) first: full tiles
   // are then ordered by falling causal length, and the local tiles that end
@@ -479,8 +505,27 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
     g_s = min(g_s, s_range[i]);
     g_e = max(g_e, s_range[kWaves + i]);
   }
-  const int t_begin = g_s / kBN;
-  const int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : t_begin;
+  int t_begin = g_s / kBN;
+  int t_end = g_e > g_s ? (g_e + kBN - 1) / kBN : t_begin;
+  // Key-range split: chunk slot k of a full item is chunk c0 + k of its
+  // tiles; slots past its last chunk do nothing.  An item whose rows span
+  // more chunks than it has slots (a sparse list over several sequences) runs
+  // whole in slot 0.  Every full item records (chunks, c0) once, from slot
+  // 0, for the merge (chunks 1: nothing to merge).
+  bool split_item = false;
+  if (kSplit && branch == 0) {
+    const int c0 = t_end > t_begin ? t_begin / kSplitTiles : 0;
+    const int c1 = t_end > t_begin ? (t_end - 1) / kSplitTiles : 0;
+    const int nch = c1 - c0 + 1 <= p.maxc ? c1 - c0 + 1 : 1;
+    if (cslot >= nch) return;   // uniform: every wave has the same range
+    split_item = nch > 1;
+    if (cslot == 0 && tid == 0) p.part_n[t * p.hkv + kvh] = make_int2(nch, c0);
+    if (split_item) {
+      const int c = c0 + cslot;
+      t_begin = max(t_begin, c * kSplitTiles);
+      t_end = min(t_end, (c + 1) * kSplitTiles);
+    }
+  }
   // Tiles inside every row's range (they skip the mask), as scalars.  (The
   // tile-skip test stays on vector registers: as a scalar condition it lets
   // the compiler restructure the step so that its registers overflow.)
@@ -545,10 +590,81 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   // free once every wave's last loads (empty descriptors) have landed and
   // every wave is past its last tile.
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  if (kSplit && split_item) {
+    // One chunk of a split item: its normalised fp32 O rows and log2 LSE
+    // (a row with no key in the chunk: O 0, LSE -inf); fwd_merge_kernel
+    // folds the chunks.  Element 4j+e of accumulator d is d-row
+    // 32d + 8j + 4hh + e of this lane's row.
+    const int64_t ps = static_cast<int64_t>(t * p.hkv + kvh) * p.maxc + cslot;
+    const int rr = wave * kRowsPerWave + rl;
+    const float inv = w.l > 0.f ? 1.0f / w.l : 0.f;
+    float* po = p.part_o + (ps * kRowsPerItem + rr) * kD + 4 * hh;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<float4*>(po + 32 * d + 8 * j) =
+            make_float4(w.o[d][4 * j] * inv, w.o[d][4 * j + 1] * inv, w.o[d][4 * j + 2] * inv,
+                        w.o[d][4 * j + 3] * inv);
+    }
+    if (hh == 0)
+      p.part_lse[ps * kRowsPerItem + rr] = w.l > 0.f ? log2f(w.l) + w.m * w.c : -INFINITY;
+    return;
+  }
   if (valid && hh == 0) p.lse[static_cast<int64_t>(pos) * p.hq + qh] = log2f(w.l) + w.m * w.c;
   store_rows_via_lds(smem + wave * kStoreRegionBytes,
                      valid ? (static_cast<int64_t>(pos) * p.hq + qh) * kD : -1, w.o, 1.0f / w.l,
                      p.out, lane);
+}
+
+// Rows of split full items: O = sum_c 2^(LSE_c - LSE) O_c and LSE = log2
+// sum_c 2^LSE_c over the item's chunks (those with LSE_c = -inf skipped; a
+// row with no key in any chunk is 0 / 0 = NaN with LSE -inf, as the unsplit
+// kernel writes it).  One thread per (full item, row, 4 of the 128 d), the
+// chunks summed in order.
+__global__ __launch_bounds__(256) void fwd_merge_kernel(const FwdParams p) {
+  const int64_t id = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int q4 = static_cast<int>(id & 31);
+  const int rr = static_cast<int>((id >> 5) & (kRowsPerItem - 1));
+  const int fi = static_cast<int>(id >> 12);   // full item = t * hkv + kvh
+  if (fi >= p.tiles[0] * p.hkv) return;
+  const int2 nc = p.part_n[fi];
+  if (nc.x <= 1) return;   // computed whole by its workgroup
+  const int t = fi / p.hkv, kvh = fi - t * p.hkv;
+  const int tile = p.tiles[0] - 1 - t;
+  const int r = tile * kRowsPerItem + rr;
+  const int G = p.group;
+  const int slot = r / G;
+  if (slot >= p.count[0]) return;
+  const int listed = p.idx[0][slot];
+  if (static_cast<uint32_t>(listed) >= static_cast<uint32_t>(p.total_q)) return;
+  const int qh = kvh * G + (r - slot * G);
+  const int64_t ps0 = static_cast<int64_t>(fi) * p.maxc;
+  float mx = -INFINITY;
+  for (int k = 0; k < nc.x; ++k) mx = fmaxf(mx, p.part_lse[(ps0 + k) * kRowsPerItem + rr]);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.f;
+  if (mx != -INFINITY) {
+    for (int k = 0; k < nc.x; ++k) {
+      const float lc = p.part_lse[(ps0 + k) * kRowsPerItem + rr];
+      if (lc == -INFINITY) continue;
+      const float wgt = exp2f(lc - mx);
+      const float4 o = reinterpret_cast<const float4*>(
+          p.part_o + ((ps0 + k) * kRowsPerItem + rr) * kD)[q4];
+      acc.x += wgt * o.x;
+      acc.y += wgt * o.y;
+      acc.z += wgt * o.z;
+      acc.w += wgt * o.w;
+      lsum += wgt;
+    }
+  }
+  const float inv = 1.0f / lsum;   // no key at all: 0 / 0 = NaN
+  uint2 u;
+  u.x = pack_bf16x2(acc.x * inv, acc.y * inv);
+  u.y = pack_bf16x2(acc.z * inv, acc.w * inv);
+  const int64_t row = static_cast<int64_t>(listed) * p.hq + qh;
+  *reinterpret_cast<uint2*>(p.out + row * kD + 4 * q4) = u;
+  if (q4 == 0) p.lse[row] = mx == -INFINITY ? -INFINITY : mx + log2f(lsum);
 }
 
 }  // namespace
@@ -558,12 +674,60 @@ using namespace swattn;
 using namespace swattn::tiles;
 
 inline int64_t kv_tiles_for(int64_t total_kv) { return ceil_div(total_kv, kBN); }
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Key-range split plan.  A full item spans up to ceil(seq_kv / 64) + 1 key
+// tiles; when that is more than one chunk and more than twice the estimated
+// tiles per workgroup slot (two per CU of a 256-CU MI355X), one long causal
+// item would set the kernel's length, so full items are split at every
+// kSplitTiles.  The estimate counts full items at half a sequence of tiles
+// and local items at their window.  Workspace after the V^T tiles: the
+// chunks' fp32 O rows, their LSE and one (chunks, first chunk) per full item.
+constexpr int64_t kSplitSlots = 512;
+struct SplitPlan {
+  int32_t maxc = 1;
+  size_t off_o = 0, off_lse = 0, off_n = 0, bytes = 0;   // offsets from the workspace start
+};
+
+inline SplitPlan split_plan(int32_t batch, int64_t seq_kv, int32_t heads_q, int32_t heads_kv,
+                            int32_t window, int64_t n_full, int64_t n_local) {
+  SplitPlan sp;
+  const int64_t group = heads_q / heads_kv;
+  const int64_t full_items = ceil_div(n_full * group, kRowsPerItem);
+  const int64_t local_items = ceil_div(n_local * group, kRowsPerItem);
+  const int64_t seq_tiles = ceil_div(seq_kv, kBN);
+  const int64_t longest = full_items > 0 ? seq_tiles + 1 : 0;
+  const int64_t local_tiles = ceil_div(std::min<int64_t>(window, seq_kv), kBN) + 2;
+  const int64_t est = heads_kv * (full_items * (seq_tiles / 2 + 2) + local_items * local_tiles);
+  if (longest <= kSplitTiles || longest <= 2 * (est / kSplitSlots)) return sp;
+  sp.maxc = static_cast<int32_t>(ceil_div(seq_tiles, kSplitTiles) + 1);
+  const size_t slots = static_cast<size_t>(full_items * heads_kv) * sp.maxc;
+  size_t o = align256(static_cast<size_t>(heads_kv) * kv_tiles_for(static_cast<int64_t>(batch) * seq_kv) *
+                      kTileBytes);
+  sp.off_o = o;   o = align256(o + slots * kRowsPerItem * kD * sizeof(float));
+  sp.off_lse = o; o = align256(o + slots * kRowsPerItem * sizeof(float));
+  sp.off_n = o;   o = align256(o + static_cast<size_t>(full_items * heads_kv) * sizeof(int2));
+  sp.bytes = o;
+  return sp;
+}
 
 extern "C" size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t heads_kv,
                                                  int32_t head_dim) {
   if (batch < 1 || seq_kv < 1 || heads_kv < 1 || head_dim != kD) return 0;
   return static_cast<size_t>(heads_kv) * kv_tiles_for(static_cast<int64_t>(batch) * seq_kv) *
          kTileBytes;
+}
+
+extern "C" size_t swattn_prefill_split_workspace_bytes(int32_t batch, int64_t seq_q,
+                                                       int64_t seq_kv, int32_t heads_q,
+                                                       int32_t heads_kv, int32_t head_dim,
+                                                       int32_t window, int64_t n_full,
+                                                       int64_t n_local) {
+  if (batch < 1 || seq_q < 0 || seq_kv < 1 || heads_q < 1 || heads_kv < 1 || head_dim != kD ||
+      heads_q % heads_kv != 0 || window <= 0 || n_full < 0 || n_local < 0)
+    return 0;
+  const SplitPlan sp = split_plan(batch, seq_kv, heads_q, heads_kv, window, n_full, n_local);
+  return sp.maxc > 1 ? sp.bytes : swattn_prefill_workspace_bytes(batch, seq_kv, heads_kv, head_dim);
 }
 
 extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
@@ -635,14 +799,36 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
   p.group = group;
   p.window = window;
   p.c = scale_log2;
-  const int64_t grid = (static_cast<int64_t>(p.tiles[0]) + p.tiles[1]) * heads_kv;
+  // The key-range split runs when the plan asks for it and the workspace is
+  // the larger size that swattn_prefill_split_workspace_bytes() returns.
+  const SplitPlan sp = split_plan(batch, seq_kv, heads_q, heads_kv, window, n_full, n_local);
+  const bool split = sp.maxc > 1 && workspace_bytes >= sp.bytes;
+  p.maxc = split ? sp.maxc : 1;
+  char* ws = static_cast<char*>(workspace);
+  p.part_o = split ? reinterpret_cast<float*>(ws + sp.off_o) : nullptr;
+  p.part_lse = split ? reinterpret_cast<float*>(ws + sp.off_lse) : nullptr;
+  p.part_n = split ? reinterpret_cast<int2*>(ws + sp.off_n) : nullptr;
+  const int64_t grid = (static_cast<int64_t>(p.tiles[0]) * p.maxc + p.tiles[1]) * heads_kv;
   if (grid > INT32_MAX) return invalid("swattn_prefill_fwd: grid too large");
   const hipStream_t st = as_stream(stream);
   hipLaunchKernelGGL(vt_pack_kernel, dim3(p.kv_tiles, heads_kv), dim3(256), 0, st, p.v,
                      static_cast<uint16_t*>(workspace), p.total_kv, heads_kv, p.kv_tiles);
-  if (meta)
-    hipLaunchKernelGGL(fwd_kernel<true>, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, st, p);
-  else
-    hipLaunchKernelGGL(fwd_kernel<false>, dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, st, p);
+  const dim3 g3(static_cast<uint32_t>(grid)), b3(kThreads);
+  if (split) {
+    if (meta)
+      hipLaunchKernelGGL((fwd_kernel<true, true>), g3, b3, 0, st, p);
+    else
+      hipLaunchKernelGGL((fwd_kernel<false, true>), g3, b3, 0, st, p);
+  } else {
+    if (meta)
+      hipLaunchKernelGGL((fwd_kernel<true, false>), g3, b3, 0, st, p);
+    else
+      hipLaunchKernelGGL((fwd_kernel<false, false>), g3, b3, 0, st, p);
+  }
+  if (split && p.tiles[0] > 0)
+    hipLaunchKernelGGL(fwd_merge_kernel,
+                       dim3(static_cast<uint32_t>(static_cast<int64_t>(p.tiles[0]) * heads_kv *
+                                                  kRowsPerItem * 32 / 256)),
+                       dim3(256), 0, st, p);
   return launch_status("swattn_prefill_fwd");
 }

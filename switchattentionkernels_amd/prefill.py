@@ -313,7 +313,11 @@ def switch_gqa_prefill_forward(
     scale = ((1.0 / dim) ** 0.5 if sm_scale is None else float(sm_scale)) * LOG2E
     md = metadata
     L = _lib.lib()
-    ws_bytes = int(L.swattn_prefill_workspace_bytes(batch, kv_len, kv_heads, dim))
+    # The larger workspace that lets the kernel split long full items by key
+    # range when they would otherwise set its length (few KV heads).
+    ws_bytes = int(L.swattn_prefill_split_workspace_bytes(batch, q_len, kv_len, heads, kv_heads,
+                                                          dim, int(window_size), full.numel(),
+                                                          local.numel()))
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     with _lib.on_device(q.device):
         st = L.swattn_prefill_fwd(

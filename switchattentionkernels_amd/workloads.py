@@ -15,6 +15,8 @@ b2     B2  S4096  Hq32/Hkv8  W1024, inputs x0.5                      Bernoulli(p
 s16k   B1  S16384 Hq32/Hkv8  W1024                                  Bernoulli(p), p in {.1, .25, .5}
 varlen 8 seqs, lengths U[512, 8192], Hq64/Hkv8, W2048               Markov(stay .95, p .3)
 s64k   B1  S65536 Hq40/Hkv8  W4096                                  ramp 0.05 -> 0.25
+kvh1   B1  S16384 Hq4/Hkv1   W1024 (one GPU's share of s16k split   Bernoulli(0.25)
+       by KV head over 8 GPUs)
 =====  ==========================================================  =========
 """
 
@@ -47,6 +49,7 @@ CONFIGS = {
     "s16k": Workload("s16k", 1, 16384, 32, 8, 1024),
     "varlen": Workload("varlen", 1, 0, 64, 8, 2048, routing="markov", p_full=0.3),
     "s64k": Workload("s64k", 1, 65536, 40, 8, 4096, routing="ramp", p_full=0.15),
+    "kvh1": Workload("kvh1", 1, 16384, 4, 1, 1024),
 }
 
 

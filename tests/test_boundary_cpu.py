@@ -34,7 +34,7 @@ def _header_functions():
 
 def test_library_exports_every_header_symbol():
     funcs = _header_functions()
-    assert len(funcs) == 16, funcs
+    assert len(funcs) == 17, funcs
     lib = _lib.lib()
     for name in funcs:
         assert hasattr(lib, name), name
@@ -66,6 +66,17 @@ def test_version_and_workspace():
     nb = 8 * (-(-(3000 * 4) // 32) + -(-(7000 * 4) // 32))
     expect_big = nb * 1024 + 256 + 2 * 64 * 2 * 4     # 64 key tiles x 8 KV heads = 512 pairs
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 64 * 256, 32, 8, 128, 3000, 7000) == expect_big
+    # key-range split of the forward: one GPU's share of config #3 split by KV
+    # head (Hq4/Hkv1) takes it, config #3 itself and config #1 do not
+    base = lib.swattn_prefill_workspace_bytes(1, 16384, 1, 128)
+    big = lib.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 4, 1, 128, 1024, 4028, 12356)
+    assert big > base
+    assert (lib.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 32, 8, 128, 1024, 4028,
+                                                     12356)
+            == lib.swattn_prefill_workspace_bytes(1, 16384, 8, 128))
+    assert (lib.swattn_prefill_split_workspace_bytes(1, 1024, 1024, 8, 2, 128, 256, 256, 768)
+            == lib.swattn_prefill_workspace_bytes(1, 1024, 2, 128))
+    assert lib.swattn_prefill_split_workspace_bytes(1, 1024, 1024, 8, 3, 128, 256, 256, 768) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 30, 8, 128, 300, 700) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 64, 300, 700) == 0
 

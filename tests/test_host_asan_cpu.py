@@ -47,6 +47,9 @@ CHILD = textwrap.dedent('''
     err(L.swattn_build_metadata(None, None, 2, 10, 10, 4, P, P, P, P, P, P, P, None), EINVAL,
         "swattn_build_metadata")
     assert L.swattn_prefill_workspace_bytes(1, 16384, 8, 128) == 8 * 256 * 16384
+    assert L.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 4, 1, 128, 1024, 4028,
+                                                  12356) > 256 * 16384
+    assert L.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 4, 1, 128, 0, 4028, 12356) == 0
     assert L.swattn_prefill_workspace_bytes(1, 16384, 8, 64) == 0
     fwd = lambda hd, hq, w, ws: L.swattn_prefill_fwd(
         P, P, P, P, 100, P, 100, None, None, None, P, P, 1, 200, 200, hq, 8, hd, w, 0.1, P, ws,
