@@ -277,18 +277,18 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *              info per KV head and 32 listed rows, plus a little (Q and dO
  *              are read in place, never copied); for fewer than 512
  *              (256-key tile, KV head) pairs also fp32 dK/dV partials of
- *              256 KiB per split workgroup (at most 256 MiB), and for fewer
- *              than 512 dQ workgroups fp32 dQ partials of 128 KiB per split
- *              workgroup (at most 128 MiB); overwritten (calls sharing it
- *              must not overlap).
+ *              256 KiB per split workgroup (at most 256 MiB), and, when the
+ *              longest dQ row tile would set that pass's length, fp32 dQ
+ *              partials of 128 KiB per piece slot (at most 320 MiB);
+ *              overwritten (calls sharing it must not overlap).
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
  * ascending positions): the keys a row block can see are found by binary
  * search over them.
  */
 size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t heads_q,
-                                          int32_t heads_kv, int32_t head_dim, int64_t n_full,
-                                          int64_t n_local);
+                                          int32_t heads_kv, int32_t head_dim, int32_t window,
+                                          int64_t n_full, int64_t n_local);
 int swattn_prefill_bwd(const void* q, const void* k, const void* v, const void* out,
                        const float* lse, const void* dout, const int32_t* full_idx,
                        int64_t n_full, const int32_t* local_idx, int64_t n_local,

@@ -39,8 +39,8 @@ SIGNATURES = {
     "swattn_prefill_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp,
                                           _vp, _vp, _i32, _i64, _i64, _i32, _i32, _i32, _i32,
                                           ctypes.c_float, _vp, ctypes.c_size_t, _vp]),
-    "swattn_prefill_bwd_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32, _i32, _i64,
-                                                             _i64]),
+    "swattn_prefill_bwd_workspace_bytes": (ctypes.c_size_t, [_i32, _i64, _i32, _i32, _i32, _i32,
+                                                             _i64, _i64]),
     "swattn_prefill_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _vp,
                                           _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i32, _i32,
                                           _i32, _i32, ctypes.c_float, _vp, ctypes.c_size_t, _vp]),

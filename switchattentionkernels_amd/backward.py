@@ -98,7 +98,8 @@ def switch_gqa_prefill_backward(
     md = metadata
     L = _lib.lib()
     ws_bytes = int(L.swattn_prefill_bwd_workspace_bytes(batch, kv_len, heads, kv_heads, dim,
-                                                        full.numel(), local.numel()))
+                                                        int(window_size), full.numel(),
+                                                        local.numel()))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     with _lib.on_device(q.device):
         st = L.swattn_prefill_bwd(

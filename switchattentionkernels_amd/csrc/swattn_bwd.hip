@@ -46,9 +46,11 @@
 // * Grids of fewer than 512 (key tile, KV head) pairs split each pair over
 //   its row blocks (up to 16 workgroups); bwd_dkdv_reduce_kernel sums the
 //   fp32 partials in split order.  Pairs run longest first (the first key
-//   tiles of each sequence are seen by the most rows).  dQ grids of fewer
-//   than 512 workgroups split each row tile over its key tiles the same
-//   way (bwd_dq_reduce_kernel).
+//   tiles of each sequence are seen by the most rows).  When the longest
+//   dQ row tile (the latest full rows see every earlier key) would set the
+//   dQ kernel's length, row tiles longer than the estimated key tiles per
+//   workgroup slot are cut into equal pieces of their key range; pieces
+//   write fp32 partials that bwd_dq_reduce_kernel sums in piece order.
 // * dQ is a separate pass (S and dP recomputed) rather than atomics from the
 //   key-stationary pass, so every output is written once, deterministically.
 
@@ -95,7 +97,7 @@ constexpr int kDkvMaxSplit = 16;
 // block d elements 4j .. 4j+3 in unit 4d + j), unit-major like the dK/dV ones.
 constexpr int kDqPartUnits = 16;
 constexpr size_t kDqPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kDqPartUnits * 64 * 16;   // 128 KiB
-constexpr int kDqMinTilesPerSplit = 4;   // 64-key tiles a dQ split takes at least
+constexpr int kDqMinTilesPerSplit = 4;   // 64-key tiles a dQ piece takes at least
 // dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
 constexpr int kQStageBytes = 2 * kTileBytes;
 
@@ -123,8 +125,10 @@ struct BwdParams {
   float* dkv_part;           // dK/dV split partials (dkv_split > 1): [workgroup][8 waves][32][64 lanes] float4
   int32_t dkv_split;         // dK/dV workgroups per (key tile, KV head), over its row blocks
   int32_t dkv_batches;       // > 1: key tiles ordered tile-in-sequence-major over this many sequences
-  float* dq_part;            // dQ split partials (dq_split > 1): [workgroup][8 waves][16][64 lanes] float4
-  int32_t dq_split;          // dQ workgroups per (branch, row tile, KV head), over its key tiles
+  float* dq_part;            // dQ piece partials (dq_chunk > 0): [workgroup][8 waves][16][64 lanes] float4
+  int32_t* dq_nch;           // pieces per (row tile, KV head), written by piece 0 (dq_chunk > 0)
+  int32_t dq_chunk;          // key tiles per dQ piece (0: row tiles are never cut)
+  int32_t dq_maxc[2];        // workgroup slots per row tile of each branch
   int32_t seq_q, seq_kv, total_q, total_kv, kv_tiles_dkv;
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
@@ -695,12 +699,15 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   // stages, its source pointer) then stay scalar selects.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 31, h = lane >> 5;
-  // Workgroup = ((row tile t, split s), KV head), KV head fastest: split s
-  // of dq_split takes an equal share of the tile's key tiles.
+  // Workgroup = ((row tile t, piece slot s), KV head), KV head fastest; a
+  // row tile of branch b has dq_maxc[b] consecutive slots.
   const int kvh = blockIdx.x % p.hkv;
   const int ts = blockIdx.x / p.hkv;
-  const int t = ts / p.dq_split;
-  const int s_idx = ts - t * p.dq_split;
+  const int full_slots = p.items[0] * p.dq_maxc[0];
+  const int t = ts < full_slots ? ts / p.dq_maxc[0]
+                                : p.items[0] + (ts - full_slots) / p.dq_maxc[1];
+  const int s_idx = ts < full_slots ? ts - t * p.dq_maxc[0]
+                                    : ts - full_slots - (t - p.items[0]) * p.dq_maxc[1];
   const int b = t < p.items[0] ? 0 : 1;
   // Latest positions first in each branch (longest rows first).
   const int item = b == 0 ? p.items[0] - 1 - t : p.items[0] + p.items[1] - 1 - t;
@@ -725,21 +732,6 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
     ke = infi[kInfoEnd + n];
     row_off = reinterpret_cast<const int64_t*>(inf)[kInfoRowOff + n];
   }
-  if (row_off >= 0) {
-    const uint16_t* qrow = p.q + row_off + 8 * h;
-    const uint16_t* drow = p.dout + row_off + 8 * h;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
-      dof[kk] = *reinterpret_cast<const bf16x8*>(drow + 16 * kk);
-    }
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qf[kk] = dof[kk] = bf16x8{};
-  }
-  // As in the dK/dV kernel: the row loads complete here, known to the
-  // compiler, so that no wait in the tile loop drains the tile LDS loads.
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   const bool has = valid && ks < ke;
   const int w_min_s = wave_min(has ? ks : INT_MAX);
   const int w_max_e = wave_max(has ? ke : INT_MIN);
@@ -756,10 +748,38 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
   const int t_all0 = g_e > g_s ? g_s / kBN : 0;
   const int t_all1 = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
-  // This split's key tiles [t_begin, t_end).
-  const int dq_chunk = (t_all1 - t_all0 + p.dq_split - 1) / p.dq_split;
-  const int t_begin = t_all0 + min(t_all1 - t_all0, s_idx * dq_chunk);
-  const int t_end = min(t_all1, t_begin + dq_chunk);
+  // This piece's key tiles [t_begin, t_end): a row tile longer than dq_chunk
+  // tiles is cut into nch (at most dq_maxc[b]) equal pieces; slots past nch
+  // have nothing to do (uniform over the workgroup: every thread computed
+  // the same range).
+  int t_begin = t_all0, t_end = t_all1;
+  bool piece = false;
+  if (p.dq_chunk > 0) {
+    const int len = t_all1 - t_all0;
+    const int nch = max(1, min(p.dq_maxc[b], (len + p.dq_chunk - 1) / p.dq_chunk));
+    if (s_idx >= nch) return;
+    if (s_idx == 0 && tid == 0) p.dq_nch[t * p.hkv + kvh] = nch;
+    piece = nch > 1;
+    const int plen = (len + nch - 1) / nch;
+    t_begin = t_all0 + min(len, s_idx * plen);
+    t_end = min(t_all1, t_begin + plen);
+  }
+  // Q and dO rows (after the exchange, so that unused piece slots load
+  // nothing).  As in the dK/dV kernel: the row loads complete here, known to
+  // the compiler, so that no wait in the tile loop drains the tile LDS loads.
+  if (row_off >= 0) {
+    const uint16_t* qrow = p.q + row_off + 8 * h;
+    const uint16_t* drow = p.dout + row_off + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      qf[kk] = *reinterpret_cast<const bf16x8*>(qrow + 16 * kk);
+      dof[kk] = *reinterpret_cast<const bf16x8*>(drow + 16 * kk);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) qf[kk] = dof[kk] = bf16x8{};
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   // Tiles inside the range of every row this wave stores need no mask.  A
   // stored row with no key (start = end = 0) must see every tile masked, so
   // it counts as start = +inf, end = -inf; lanes that store nothing do not
@@ -861,9 +881,9 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
 
   const int G = p.group;
-  if (p.dq_split > 1) {
-    // fp32 partials (zeros for a split with no tiles); bwd_dq_reduce_kernel
-    // sums the splits in order and stores the rows.
+  if (piece) {
+    // fp32 partials (zeros for a piece with no tiles); bwd_dq_reduce_kernel
+    // sums the pieces in order and stores the rows.
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
 #pragma unroll
@@ -891,9 +911,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
 }
 
-// dQ of split row tiles: one thread per (row tile and KV head, wave, float4
-// unit, lane).  It sums that unit over the splits in split order
-// (deterministic) and stores its four bf16 values where the unsplit kernel
+// dQ of row tiles cut into pieces: one thread per (row tile and KV head,
+// wave, float4 unit, lane); row tiles left whole were stored by the dQ
+// kernel.  It sums that unit over the pieces in piece order
+// (deterministic) and stores its four bf16 values where a whole row tile
 // would: the lane's row of the tile, d-rows 32d + 8j + 4h .. +3.
 static_assert(kDqPartUnits == 16 && kBwdWaves == 8, "the reduce's thread index splits 6 + 4 + 3 bits");
 __global__ __launch_bounds__(kThreads) void bwd_dq_reduce_kernel(const BwdParams p) {
@@ -903,9 +924,16 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce_kernel(const BwdParams
   const int wave = static_cast<int>((id >> 10) & (kBwdWaves - 1));
   const int tk = static_cast<int>(id >> 13);   // (row tile t, KV head), KV head fastest
   const int kvh = tk % p.hkv, t = tk / p.hkv;
+  const int nch = p.dq_nch[tk];
+  if (nch <= 1) return;
+  // The row tile's first workgroup slot (slots are ordered as the dQ grid).
+  const int64_t slot0 = t < p.items[0]
+                            ? static_cast<int64_t>(t) * p.dq_maxc[0]
+                            : static_cast<int64_t>(p.items[0]) * p.dq_maxc[0] +
+                                  static_cast<int64_t>(t - p.items[0]) * p.dq_maxc[1];
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp = 0; sp < p.dq_split; ++sp) {
-    const int64_t wg = (static_cast<int64_t>(t) * p.dq_split + sp) * p.hkv + kvh;
+  for (int sp = 0; sp < nch; ++sp) {
+    const int64_t wg = (slot0 + sp) * p.hkv + kvh;
     const float4 a = *dq_part_unit(p, wg, wave, u, lane);
     acc.x += a.x;
     acc.y += a.y;
@@ -934,14 +962,14 @@ __global__ __launch_bounds__(kThreads) void bwd_dq_reduce_kernel(const BwdParams
 // Host side.
 // ---------------------------------------------------------------------------
 struct BwdLayout {
-  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv, dkv_split, dq_split;
-  size_t off_info, off_zero, off_ranges, off_part, off_dq_part, bytes;
+  int64_t blocks[2], items[2], total_blocks, kv_tiles_dkv, dkv_split, dq_chunk, dq_maxc[2];
+  size_t off_info, off_zero, off_ranges, off_part, off_dq_nch, off_dq_part, bytes;
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, int64_t group,
-                            int64_t n_full, int64_t n_local) {
+                            int32_t window, int64_t n_full, int64_t n_local) {
   BwdLayout L{};
   const int64_t n[2] = {n_full, n_local};
   for (int b = 0; b < 2; ++b) {
@@ -962,18 +990,43 @@ inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, 
   L.off_ranges = o; o = align256(o + static_cast<size_t>(2 * L.kv_tiles_dkv) * 2 * sizeof(int32_t));
   L.off_part = o;
   if (L.dkv_split > 1) o += static_cast<size_t>(pairs * L.dkv_split) * kPartBytesPerWg;
-  // dQ likewise: fewer row tiles (times KV heads) than two rounds of
-  // workgroups, each split over its key tiles, at least
-  // kDqMinTilesPerSplit of the longest possible range (one sequence's keys)
-  // per split.
+  // dQ: a row tile's key tiles, estimated per branch (a full row tile of
+  // one sequence spans up to a sequence's keys, half of them on average; a
+  // local one about a window).  When the longest one exceeds twice the
+  // estimated tiles per workgroup slot (the sum over kDkvTargetWgs slots),
+  // row tiles are cut into pieces of at most twice that many tiles (at
+  // least kDqMinTilesPerSplit), so that the longest no longer sets the
+  // kernel's length.  (Measured on the KV-head share of a 16K-token,
+  // 4-query-head prefill: pieces of 1x, 1.25x, 1.5x, 3x and 4x the
+  // per-slot tiles all ran 5-15% slower than 2x, which pairs a long piece
+  // with a short row tile on a CU.)  Each row tile has room for as many
+  // pieces as its branch's longest estimate needs.
   const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
-  const int64_t max_tiles = ceil_div(seq_kv, kBN) + 1;
-  L.dq_split = 1;
-  if (q_items > 0 && q_items < kDkvTargetWgs)
-    L.dq_split = std::max<int64_t>(1, std::min<int64_t>({kDkvMaxSplit, ceil_div(kDkvTargetWgs, q_items),
-                                                         max_tiles / kDqMinTilesPerSplit}));
+  const int64_t full_len = ceil_div(seq_kv, kBN) + 1;
+  const int64_t local_len = std::min<int64_t>(full_len, ceil_div(window, kBN) + 2);
+  const int64_t est = heads_kv * (L.items[0] * (full_len / 2 + 1) + L.items[1] * local_len);
+  const int64_t per_slot = ceil_div(est, kDkvTargetWgs);
+  const int64_t longest = L.items[0] > 0 ? full_len : local_len;
+  L.dq_chunk = 0;
+  L.dq_maxc[0] = L.dq_maxc[1] = 1;
+  if (q_items > 0 && longest > 2 * per_slot && longest > kDqMinTilesPerSplit) {
+    L.dq_chunk = std::max<int64_t>(kDqMinTilesPerSplit, 2 * per_slot);
+    L.dq_maxc[0] = ceil_div(full_len, L.dq_chunk);
+    L.dq_maxc[1] = ceil_div(local_len, L.dq_chunk);
+  }
+  // Partials are indexed by the dQ workgroup; full row tiles' slots come
+  // first, and local ones are only cut when their branch has more than one
+  // slot.  With the rule above fewer than 512 (row tile, KV head) pairs of a
+  // branch can be cut, each into fewer than its estimate / per_slot + 1
+  // pieces: under 1536 full and 1024 local slots, 320 MiB.
+  L.off_dq_nch = o;
   L.off_dq_part = o;
-  if (L.dq_split > 1) o += static_cast<size_t>(q_items * L.dq_split) * kDqPartBytesPerWg;
+  if (L.dq_chunk > 0) {
+    o = align256(o + static_cast<size_t>(q_items) * sizeof(int32_t));
+    L.off_dq_part = o;
+    const int64_t slots = L.items[0] * L.dq_maxc[0] + (L.dq_maxc[1] > 1 ? L.items[1] * L.dq_maxc[1] : 0);
+    o += static_cast<size_t>(heads_kv * slots) * kDqPartBytesPerWg;
+  }
   L.bytes = o;
   return L;
 }
@@ -986,13 +1039,13 @@ using namespace swattn::tiles;
 
 extern "C" size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_kv,
                                                      int32_t heads_q, int32_t heads_kv,
-                                                     int32_t head_dim, int64_t n_full,
-                                                     int64_t n_local) {
+                                                     int32_t head_dim, int32_t window,
+                                                     int64_t n_full, int64_t n_local) {
   if (batch < 1 || seq_kv < 1 || heads_q < 1 || heads_kv < 1 || head_dim != kD ||
-      heads_q % heads_kv != 0 || n_full < 0 || n_local < 0)
+      heads_q % heads_kv != 0 || window <= 0 || n_full < 0 || n_local < 0)
     return 0;
   const BwdLayout L = bwd_layout(seq_kv, static_cast<int64_t>(batch) * seq_kv, heads_kv,
-                                 heads_q / heads_kv, n_full, n_local);
+                                 heads_q / heads_kv, window, n_full, n_local);
   return L.bytes;
 }
 
@@ -1041,13 +1094,14 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
       (n_full + n_local > 0 &&
        (!aligned16(q) || !aligned16(out) || !aligned16(dout) || !aligned16(dq))))
     return invalid("swattn_prefill_bwd: q, k, v, out, dout, dq, dk and dv must be 16-byte aligned");
-  const BwdLayout L = bwd_layout(seq_kv, total_kv, heads_kv, group, n_full, n_local);
+  const BwdLayout L = bwd_layout(seq_kv, total_kv, heads_kv, group, window, n_full, n_local);
   if (workspace == nullptr || workspace_bytes < L.bytes) {
     set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
     return SWATTN_EWORKSPACE;
   }
-  if (L.kv_tiles_dkv * heads_kv > INT32_MAX ||
-      (L.items[0] + L.items[1]) * heads_kv > INT32_MAX)
+  if (L.kv_tiles_dkv * heads_kv * L.dkv_split > INT32_MAX ||
+      (L.items[0] * L.dq_maxc[0] + L.items[1] * L.dq_maxc[1]) * heads_kv > INT32_MAX ||
+      (L.items[0] + L.items[1]) * heads_kv * kBwdWaves * kDqPartUnits * 64 / kThreads > INT32_MAX)
     return invalid("swattn_prefill_bwd: grid too large");
 
   char* ws = static_cast<char*>(workspace);
@@ -1087,7 +1141,10 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   // Several sequences that each hold whole 256-key tiles: interleave them.
   p.dkv_batches = (batch > 1 && seq_kv % kKeysDkv == 0) ? batch : 1;
   p.dkv_part = reinterpret_cast<float*>(ws + L.off_part);
-  p.dq_split = static_cast<int32_t>(L.dq_split);
+  p.dq_chunk = static_cast<int32_t>(L.dq_chunk);
+  p.dq_maxc[0] = static_cast<int32_t>(L.dq_maxc[0]);
+  p.dq_maxc[1] = static_cast<int32_t>(L.dq_maxc[1]);
+  p.dq_nch = reinterpret_cast<int32_t*>(ws + L.off_dq_nch);
   p.dq_part = reinterpret_cast<float*>(ws + L.off_dq_part);
   p.hq = heads_q;
   p.hkv = heads_kv;
@@ -1120,9 +1177,10 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
                        dim3(kThreads), 0, st, p);
   const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
   if (q_items > 0) {
-    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(q_items * L.dq_split)),
-                       dim3(kBwdThreads), 0, st, p);
-    if (L.dq_split > 1)
+    const int64_t dq_wgs = (L.items[0] * L.dq_maxc[0] + L.items[1] * L.dq_maxc[1]) * heads_kv;
+    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(dq_wgs)), dim3(kBwdThreads), 0,
+                       st, p);
+    if (L.dq_chunk > 0)
       hipLaunchKernelGGL(bwd_dq_reduce_kernel,
                          dim3(static_cast<uint32_t>(q_items * kBwdWaves * kDqPartUnits * 64 / kThreads)),
                          dim3(kThreads), 0, st, p);

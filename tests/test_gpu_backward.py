@@ -232,6 +232,52 @@ def test_s16k_backward_identities_and_sampled_rows():
     _grad_close(dq, rq, "s16k dq sampled rows", rows=torch.as_tensor(rows))
 
 
+@pytest.mark.parametrize("b,s,hq,hkv,w,p", [
+    (1, 4096, 4, 1, 256, 0.3),    # dQ pieces of 4 key tiles: full row tiles in up to 17,
+                                  # local ones (6 tiles) in 2
+    (2, 2000, 8, 1, 700, 0.6),    # two sequences, pieces of 8: full in up to 5, local in 2
+])
+def test_backward_dq_pieces_match_oracle(b, s, hq, hkv, w, p):
+    """Few row tiles (one KV head): the longest dQ row tiles are cut into
+    pieces whose fp32 partials are summed in piece order."""
+    q, k, v, do = _qkv(b * 77 + s, b, s, hq, hkv)
+    m = _mask(s + 7, (b, s), p)
+    dq, dk, dv = _run(q, k, v, do, m, w)
+    rq, rk, rv = _oracle(q, k, v, do, m, w)
+    tag = f"pieces b{b} s{s} {hq}/{hkv} w{w} p{p}"
+    _grad_close(dq, rq, tag + " dq")
+    _grad_close(dk, rk, tag + " dk")
+    _grad_close(dv, rv, tag + " dv")
+    # the latest full rows see every earlier key: their row tiles are cut the most
+    f_np, _ = R.compact(m.numpy())
+    late = torch.as_tensor(f_np[-64:])
+    _grad_close(dq, rq, tag + " dq late full rows", rows=late)
+
+
+def test_kv_head_share_backward():
+    """One GPU's share of config #3 under a KV-head split (Hq4/Hkv1, S=16384,
+    W1024, p_full 0.25): dQ row tiles are cut into pieces.  Sampled dq rows
+    (late full rows included) against the oracle, dk / dv by the identities
+    of the config #3 test."""
+    wl = workloads.build("kvh1", seed=2)
+    q, k, v, m, w = wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"]
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    dq, dk, dv = _run(q, k, v, do, m, w)
+    s, hq, hkv = q.shape[1], q.shape[2], k.shape[2]
+    g = hq // hkv
+    dk32 = dk[0].float()
+    assert (dk32.sum(0).abs() <= 2e-3 * dk32.abs().sum(0) + 1e-3).all()
+    dv_sum = dv[0].float().sum(0).cpu()
+    ref = do[0].float().reshape(s, hkv, g, 128).sum((0, 2))
+    assert ((dv_sum - ref).abs() <= 2e-3 * do[0].float().abs().reshape(s, hkv, g, 128)
+            .sum((0, 2)) + 1e-2).all()
+    f_np, _ = R.compact(m.numpy())
+    rows = np.unique(np.concatenate([np.random.default_rng(2).choice(s, 256, replace=False),
+                                     f_np[-96:], [0, s - 1]]))
+    rq, _, _ = _oracle(q, k, v, do, m, w, rows=rows)
+    _grad_close(dq, rq, "kvh1 dq sampled rows", rows=torch.as_tensor(rows))
+
+
 def test_backward_with_no_query_rows():
     """No query rows: dq is empty and every key gets dk = dv = 0."""
     q = torch.zeros(1, 0, 4, 128, dtype=torch.bfloat16, device=DEV)

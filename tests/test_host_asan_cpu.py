@@ -60,8 +60,9 @@ CHILD = textwrap.dedent('''
     err(fwd(128, 32, 64, 16), EWS, "swattn_prefill_fwd")
     err(L.swattn_prefill_fwd(P, P, P, P, 100, P, 100, P, None, None, P, P, 1, 200, 200, 32, 8,
                              128, 64, 0.1, P, 1 << 30, None), EINVAL, "swattn_prefill_fwd")
-    wsb = L.swattn_prefill_bwd_workspace_bytes(1, 200, 32, 8, 128, 100, 100)
-    assert wsb > 0 and L.swattn_prefill_bwd_workspace_bytes(1, 200, 32, 8, 64, 100, 100) == 0
+    wsb = L.swattn_prefill_bwd_workspace_bytes(1, 200, 32, 8, 128, 64, 100, 100)
+    assert wsb > 0 and L.swattn_prefill_bwd_workspace_bytes(1, 200, 32, 8, 64, 64, 100, 100) == 0
+    assert L.swattn_prefill_bwd_workspace_bytes(1, 200, 32, 8, 128, -1, 100, 100) == 0
     bwd = lambda hd, ws: L.swattn_prefill_bwd(
         P, P, P, P, P, P, P, 100, P, 100, None, None, None, P, P, P, 1, 200, 200, 32, 8, hd, 64,
         0.1, P, ws, None)
