@@ -130,8 +130,9 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
  * by key range; no counterpart in the reference, whose grid is one CTA per
  * query tile and head (V:402-445).  When the longest full item (a causal row
  * tile late in a sequence) is long against the rest of the work, as with few
- * KV heads (one GPU's share of a KV-head split), a workgroup per 2048-key
- * chunk and a merge of the chunks by their log2 LSE (V:236-241) keep it from
+ * KV heads (one GPU's share of a KV-head split) or short sequences on few
+ * heads, a workgroup per chunk of 4 to 32 key tiles (planned from the shape)
+ * and a merge of the chunks by their log2 LSE (V:236-241) keep it from
  * setting the kernel's length.  Returns swattn_prefill_workspace_bytes() when
  * no split would run, a larger size (fp32 partial rows of the split items)
  * when it would, 0 for an unsupported shape.  The forward splits only if it

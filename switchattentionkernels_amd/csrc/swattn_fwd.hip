@@ -59,11 +59,12 @@
 //   mask.
 // * Key-range split (fwd_kernel<., true>, host plan in split_plan): when the
 //   longest causal item is long against the rest of the work (few KV heads,
-//   e.g. one GPU's share of a KV-head split), each full item runs as one
-//   workgroup per 2048-key chunk of its range.  The chunks' fp32 O rows and
+//   e.g. one GPU's share of a KV-head split, or short sequences on few
+//   heads), each full item runs as one workgroup per chunk of its range
+//   (4 to 32 key tiles, planned per call).  The chunks' fp32 O rows and
 //   LSE go to the workspace and fwd_merge_kernel folds them (log2 LSE,
-//   V:236-241).  Chunk boundaries are fixed multiples of 2048 keys, and an
-//   item inside one chunk is computed exactly as without a split.
+//   V:236-241).  Chunk boundaries are fixed multiples of the chunk size,
+//   and an item inside one chunk is computed exactly as without a split.
 
 #include <limits.h>
 #include <math.h>
@@ -113,17 +114,20 @@ struct FwdParams {
   int32_t hq, hkv, group, window;
   float c;                   // sm_scale * log2(e)
   // Key-range split of full items (maxc > 1): a full item whose key tiles
-  // cross a multiple of kSplitTiles runs as one workgroup per such chunk.
+  // cross a multiple of split_tiles runs as one workgroup per such chunk.
   int32_t maxc;              // chunk slots per full item (1: no split)
+  int32_t split_tiles;       // chunk size in 64-key tiles (maxc > 1)
   float* part_o;             // [full item][slot][128 rows][128] fp32 O of the chunk (normalised)
   float* part_lse;           // [full item][slot][128 rows] log2 LSE of the chunk (-inf: no key)
   int2* part_n;              // [full item] (chunks, first chunk); chunks > 1: merge needed
 };
 
-// Chunk of the key-range split, in 64-key tiles (2048 keys).  Boundaries sit
-// at fixed multiples of it, so a row's chunks depend only on its own range,
-// and an item inside one chunk is computed exactly as without a split.
+// Chunk of the key-range split, in 64-key tiles: between kSplitMinTiles and
+// kSplitTiles (2048 keys), chosen per call.  Boundaries sit at fixed
+// multiples of it, so a row's chunks depend only on its own range, and an
+// item inside one chunk is computed exactly as without a split.
 constexpr int kSplitTiles = 32;
+constexpr int kSplitMinTiles = 4;
 
 // Per-lane staging plan for one 64-key tile (constant across tiles): K rows
 // and V^T rows go 1 KiB (one lane-linear load) at a time; each wave stages
@@ -514,16 +518,16 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kThreads, kThreads),
   // 0, for the merge (chunks 1: nothing to merge).
   bool split_item = false;
   if (kSplit && branch == 0) {
-    const int c0 = t_end > t_begin ? t_begin / kSplitTiles : 0;
-    const int c1 = t_end > t_begin ? (t_end - 1) / kSplitTiles : 0;
+    const int c0 = t_end > t_begin ? t_begin / p.split_tiles : 0;
+    const int c1 = t_end > t_begin ? (t_end - 1) / p.split_tiles : 0;
     const int nch = c1 - c0 + 1 <= p.maxc ? c1 - c0 + 1 : 1;
     if (cslot >= nch) return;   // uniform: every wave has the same range
     split_item = nch > 1;
     if (cslot == 0 && tid == 0) p.part_n[t * p.hkv + kvh] = make_int2(nch, c0);
     if (split_item) {
       const int c = c0 + cslot;
-      t_begin = max(t_begin, c * kSplitTiles);
-      t_end = min(t_end, (c + 1) * kSplitTiles);
+      t_begin = max(t_begin, c * p.split_tiles);
+      t_end = min(t_end, (c + 1) * p.split_tiles);
     }
   }
   // Tiles inside every row's range (they skip the mask), as scalars.  (The
@@ -677,15 +681,18 @@ inline int64_t kv_tiles_for(int64_t total_kv) { return ceil_div(total_kv, kBN); 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 // Key-range split plan.  A full item spans up to ceil(seq_kv / 64) + 1 key
-// tiles; when that is more than one chunk and more than twice the estimated
-// tiles per workgroup slot (two per CU of a 256-CU MI355X), one long causal
-// item would set the kernel's length, so full items are split at every
-// kSplitTiles.  The estimate counts full items at half a sequence of tiles
-// and local items at their window.  Workspace after the V^T tiles: the
-// chunks' fp32 O rows, their LSE and one (chunks, first chunk) per full item.
+// tiles; when that is more than twice the estimated tiles per workgroup slot
+// (two per CU of a 256-CU MI355X), one long causal item would set the
+// kernel's length, so full items are split into chunks of twice that
+// estimate, clamped to [kSplitMinTiles, kSplitTiles] (an item must span at
+// least two chunks).  The estimate counts full items at half a sequence of
+// tiles and local items at their window.  Workspace after the V^T tiles:
+// the chunks' fp32 O rows, their LSE and one (chunks, first chunk) per full
+// item.
 constexpr int64_t kSplitSlots = 512;
 struct SplitPlan {
   int32_t maxc = 1;
+  int32_t tiles = kSplitTiles;
   size_t off_o = 0, off_lse = 0, off_n = 0, bytes = 0;   // offsets from the workspace start
 };
 
@@ -699,8 +706,11 @@ inline SplitPlan split_plan(int32_t batch, int64_t seq_kv, int32_t heads_q, int3
   const int64_t longest = full_items > 0 ? seq_tiles + 1 : 0;
   const int64_t local_tiles = ceil_div(std::min<int64_t>(window, seq_kv), kBN) + 2;
   const int64_t est = heads_kv * (full_items * (seq_tiles / 2 + 2) + local_items * local_tiles);
-  if (longest <= kSplitTiles || longest <= 2 * (est / kSplitSlots)) return sp;
-  sp.maxc = static_cast<int32_t>(ceil_div(seq_tiles, kSplitTiles) + 1);
+  const int64_t per_slot = est / kSplitSlots;
+  const int64_t chunk = std::min<int64_t>(kSplitTiles, std::max<int64_t>(kSplitMinTiles, 2 * per_slot));
+  if (longest < 2 * chunk || longest <= 2 * per_slot) return sp;
+  sp.tiles = static_cast<int32_t>(chunk);
+  sp.maxc = static_cast<int32_t>(ceil_div(seq_tiles, chunk) + 1);
   const size_t slots = static_cast<size_t>(full_items * heads_kv) * sp.maxc;
   size_t o = align256(static_cast<size_t>(heads_kv) * kv_tiles_for(static_cast<int64_t>(batch) * seq_kv) *
                       kTileBytes);
@@ -804,6 +814,7 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
   const SplitPlan sp = split_plan(batch, seq_kv, heads_q, heads_kv, window, n_full, n_local);
   const bool split = sp.maxc > 1 && workspace_bytes >= sp.bytes;
   p.maxc = split ? sp.maxc : 1;
+  p.split_tiles = sp.tiles;
   char* ws = static_cast<char*>(workspace);
   p.part_o = split ? reinterpret_cast<float*>(ws + sp.off_o) : nullptr;
   p.part_lse = split ? reinterpret_cast<float*>(ws + sp.off_lse) : nullptr;

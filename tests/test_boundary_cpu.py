@@ -84,15 +84,24 @@ def test_version_and_workspace():
     assert (lib.swattn_prefill_bwd_workspace_bytes(1, 16384, 4, 1, 128, 1024, 4028, 12356)
             == expect_kvh1)
     # key-range split of the forward: one GPU's share of config #3 split by KV
-    # head (Hq4/Hkv1) takes it, config #3 itself and config #1 do not
+    # head (Hq4/Hkv1) takes it (chunks of 32 tiles, 9 slots per full item),
+    # config #3 itself does not
     base = lib.swattn_prefill_workspace_bytes(1, 16384, 1, 128)
     big = lib.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 4, 1, 128, 1024, 4028, 12356)
     assert big > base
     assert (lib.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 32, 8, 128, 1024, 4028,
                                                      12356)
             == lib.swattn_prefill_workspace_bytes(1, 16384, 8, 128))
+    # config #1 (8 full and 24 local items of 128 rows, 2 KV heads): estimate
+    # 2 * (8 * (16 // 2 + 2) + 24 * (256 / 64 + 2)) = 448 tiles, 0 per slot of
+    # 512, so chunks of the minimum 4 tiles; the longest item (17 tiles) spans
+    # two or more, and each full item gets ceil(16 / 4) + 1 = 5 slots.  After
+    # the V^T tiles (2 x 16 tiles x 16 KiB): fp32 O rows (128 x 128) and LSE
+    # (128) per slot, one int2 per full item, each part 256-byte aligned.
+    slots = 8 * 2 * 5
+    expect1 = 2 * 16 * 16384 + slots * 128 * 128 * 4 + slots * 128 * 4 + 256
     assert (lib.swattn_prefill_split_workspace_bytes(1, 1024, 1024, 8, 2, 128, 256, 256, 768)
-            == lib.swattn_prefill_workspace_bytes(1, 1024, 2, 128))
+            == expect1)
     assert lib.swattn_prefill_split_workspace_bytes(1, 1024, 1024, 8, 3, 128, 256, 256, 768) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 30, 8, 128, 256, 300, 700) == 0
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 64, 256, 300, 700) == 0

@@ -392,39 +392,74 @@ def test_routed_equals_rowwise_select_s16k():
     assert torch.equal(lse, torch.where(md[..., None], lse_f, lse_l))
 
 
+def _unsplit_run(q, k, v, mask, window, metadata=None):
+    """swattn_prefill_fwd through the C ABI with the plain workspace
+    (swattn_prefill_workspace_bytes), which never splits items by key range:
+    every row is then one pass over its tiles in order, whatever else is in
+    the call."""
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    b, s, hq, _ = q.shape
+    skv, hkv = k.shape[1], k.shape[2]
+    L = _lib.lib()
+    ws_bytes = L.swattn_prefill_workspace_bytes(b, skv, hkv, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=DEV)
+    md = metadata
+    st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(),
+                              full.numel(), local.data_ptr(), local.numel(),
+                              _lib.ptr(md.full_starts) if md is not None else None,
+                              _lib.ptr(md.local_starts) if md is not None else None,
+                              _lib.ptr(md.causal_ends) if md is not None else None,
+                              out.data_ptr(), lse.data_ptr(), b, s, skv, hq, hkv, 128, window,
+                              ctypes.c_float(128 ** -0.5 * oracle.LOG2E), ws.data_ptr(),
+                              ws_bytes, _lib.stream_handle(q.device))
+    assert st == 0, L.swattn_last_error()
+    torch.cuda.synchronize()
+    return out, lse
+
+
 def test_batch_rows_independent():
-    """Batch rows are independent sequences.  With Skv a multiple of the 64-key
-    tile every row meets the same tiles either way, so results are bit-exact;
-    otherwise they agree to rounding."""
+    """Batch rows are independent sequences.  Without the key-range split
+    and with Skv a multiple of the 64-key tile, every row meets the same tiles
+    in the same order either way, so results are bit-exact; otherwise (and
+    through the public API, which may split long items of these small grids
+    differently for different batch sizes) they agree to rounding."""
     for s, exact in ((1024, True), (1000, False)):
         q, k, v = _qkv(6, 3, s, 8, 2)
         m = _mask(6, (3, s), 0.3)
         o, lse, _, _ = _gpu_run(q, k, v, m, 128)
+        ou, lu = _unsplit_run(q, k, v, m, 128)
         for b in range(3):
             ob, lb, _, _ = _gpu_run(q[b:b + 1], k[b:b + 1], v[b:b + 1], m[b:b + 1], 128)
+            _assert_close(o[b:b + 1], lse[b:b + 1], ob.float().cpu(), lb.cpu(),
+                          tag=f"batch row {b} vs alone")
             if exact:
-                assert torch.equal(o[b:b + 1], ob) and torch.equal(lse[b:b + 1], lb)
-            else:
-                _assert_close(o[b:b + 1], lse[b:b + 1], ob.float().cpu(), lb.cpu(),
-                              tag=f"batch row {b} vs alone")
+                oub, lub = _unsplit_run(q[b:b + 1], k[b:b + 1], v[b:b + 1], m[b:b + 1], 128)
+                assert torch.equal(ou[b:b + 1], oub) and torch.equal(lu[b:b + 1], lub)
 
 
 def test_packed_equals_per_sequence():
-    """Packed sequences never see each other: bit-exact with 64-aligned offsets,
-    equal to rounding otherwise."""
+    """Packed sequences never see each other: bit-exact with 64-aligned offsets
+    without the key-range split, equal to rounding otherwise (and through the
+    public API, whose split of these small grids depends on the shape)."""
     for cu, exact in (([0, 704, 768, 2048, 2368], True), ([0, 700, 701, 2000, 2345], False)):
         q, k, v = _qkv(7, 1, cu[-1], 8, 2)
         m = _mask(7, (1, cu[-1]), 0.3)
         full, local = build_switch_query_indices(m.to(DEV))
         o, lse = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
                                                    cu, window_size=100)
+        md = build_switch_attention_metadata(cu[-1], cu[-1], device=DEV, window_size=100,
+                                             cu_seqlens=cu)
+        ou, lu = _unsplit_run(q, k, v, m, 100, metadata=md)
         for a, b in zip(cu[:-1], cu[1:]):
             os_, ls_, _, _ = _gpu_run(q[:, a:b], k[:, a:b], v[:, a:b], m[:, a:b], 100)
+            _assert_close(o[:, a:b], lse[:, a:b], os_.float().cpu(), ls_.cpu(),
+                          tag=f"segment {a}:{b} vs alone")
             if exact:
-                assert torch.equal(o[:, a:b], os_) and torch.equal(lse[:, a:b], ls_)
-            else:
-                _assert_close(o[:, a:b], lse[:, a:b], os_.float().cpu(), ls_.cpu(),
-                              tag=f"segment {a}:{b} vs alone")
+                ous, lus = _unsplit_run(q[:, a:b], k[:, a:b], v[:, a:b], m[:, a:b], 100)
+                assert torch.equal(ou[:, a:b], ous) and torch.equal(lu[:, a:b], lus)
 
 
 def test_default_equals_explicit_metadata_bit_exact():

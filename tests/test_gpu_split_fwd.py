@@ -1,8 +1,9 @@
 """The forward's key-range split of long full items (few KV heads, long
 sequences), against the oracle and against the unsplit kernel.
 
-swattn_prefill_fwd splits full items at every 2048 keys when the longest one
-would set the kernel's length and the caller passes the workspace that
+swattn_prefill_fwd splits full items into chunks of 4 to 32 key tiles (at
+fixed multiples of the chunk size) when the longest one would set the
+kernel's length and the caller passes the workspace that
 swattn_prefill_split_workspace_bytes() asks for; the chunks are merged by
 their log2 LSE (V:236-241).  Checked here:
 
@@ -56,6 +57,20 @@ def _abi_forward(q, k, v, full, local, window, split):
     return out, lse, base, big
 
 
+def _split_tiles(s, hq, hkv, w, n_full, n_local):
+    """The chunk size (64-key tiles) of the library's split plan: twice the
+    estimated key tiles per workgroup slot (full items at half a sequence,
+    local ones at their window, over 512 slots), clamped to [4, 32].  Used
+    only to pick the rows that must come out bit-identical; a wrong value
+    here would fail the equality below."""
+    g = hq // hkv
+    full_items, local_items = -(-n_full * g // 128), -(-n_local * g // 128)
+    seq_tiles = -(-s // 64)
+    local_tiles = -(-min(w, s) // 64) + 2
+    est = hkv * (full_items * (seq_tiles // 2 + 2) + local_items * local_tiles)
+    return min(32, max(4, 2 * (est // 512)))
+
+
 def _case(seed, b, s, hq, hkv, p):
     gen = torch.Generator().manual_seed(seed)
     q, k, v = workloads.make_qkv(gen, b, s, s, hq, hkv, 128)
@@ -64,8 +79,11 @@ def _case(seed, b, s, hq, hkv, p):
 
 
 @pytest.mark.parametrize("b,s,hq,hkv,w,p", [
-    (1, 8192, 4, 1, 1024, 0.25),    # longest full item 128 tiles: split into up to 5 chunks
-    (2, 6000, 2, 1, 300, 0.5),      # two sequences, items inside one chunk and across several
+    (1, 8192, 4, 1, 1024, 0.25),    # longest full item 129 tiles: chunks of 30 tiles
+    (2, 6000, 2, 1, 300, 0.5),      # two sequences, chunks of 20 tiles: items inside one
+                                    # chunk and across several
+    (1, 1024, 8, 2, 256, 0.25),     # config #1's shape: about 64 items on 256 CUs, chunks
+                                    # of 4 tiles
 ])
 def test_split_matches_oracle_and_unsplit(b, s, hq, hkv, w, p):
     q, k, v, mask = _case(31 + s, b, s, hq, hkv, p)
@@ -76,18 +94,19 @@ def test_split_matches_oracle_and_unsplit(b, s, hq, hkv, w, p):
     print(f"split b{b} s{s} {hq}/{hkv}: workspace {base} -> {big}", flush=True)
     assert not torch.isnan(o_s).any() and not torch.isnan(l_s).any(), "a row was never written"
     o_u, l_u, _, _ = _abi_forward(qd, kd, vd, full, local, w, split=False)
-    # rows of full items that lie inside one 2048-key chunk, and every local row, are
+    # rows of full items that lie inside one chunk, and every local row, are
     # computed exactly as unsplit; late causal rows differ by rounding only
     f_np, l_np = R.compact(mask.numpy())
     # A full item (128 rows = 128 / G listed positions, head fastest) lies inside one
     # chunk when its rows' keys [b*s, b*s + i + 1), in flattened key coordinates, start
-    # and end in the same 32-tile chunk, counted as the kernel counts them.
+    # and end in the same chunk, counted as the kernel counts them.
     one_chunk = np.ones(b * s, dtype=bool)
     g = hq // hkv
+    ct = _split_tiles(s, hq, hkv, w, f_np.size, l_np.size)
     for it in range(-(-f_np.size * g // 128)):
         sl = f_np[(128 * it) // g:min((128 * it + 127) // g, f_np.size - 1) + 1]
         lo, hi = int((sl // s * s).min()), int((sl // s * s + sl % s + 1).max())
-        c0, c1 = (lo // 64) // 32, ((hi + 63) // 64 - 1) // 32
+        c0, c1 = (lo // 64) // ct, ((hi + 63) // 64 - 1) // ct
         one_chunk[sl] = c0 == c1
     ok = torch.as_tensor(one_chunk)
     assert ok.any() and not ok.all()
