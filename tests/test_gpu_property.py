@@ -1,8 +1,9 @@
 """Property-based sweeps over small shapes (hypothesis): the HIP forward, the
 HIP backward, packed sequences (forward and backward), the compaction (from
 a mask and from router logits), the routed decode, split-then-merged key
-ranges, the forward on arbitrary caller key bounds and the backward on
-monotone caller key bounds, against the CPU oracle.
+ranges, the forward on arbitrary caller key bounds, the backward on
+monotone caller key bounds, and small grids that take the forward's
+key-range split and the backward's dQ pieces, against the CPU oracle.
 
 The examples are derandomized: every run draws the same fixed set of shapes
 (batch, lengths, head counts, group size, window, routing density, key
@@ -316,5 +317,63 @@ def test_backward_monotone_bounds_property(c):
     refs = oracle.routed_attention_backward(
         q, k, v, do, f_np, l_np,
         metadata={"full_starts": fs, "local_starts": ls, "causal_ends": ce})
+    for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
+        _grad_close(g, r, f"{tag} {name}")
+
+
+split_case = st.fixed_dictionaries({
+    "b": st.integers(1, 2),
+    "s": st.integers(520, 1800),
+    "dkv": st.integers(-300, 300),
+    "hkv": st.integers(1, 2),
+    "g": st.sampled_from([1, 2, 4, 8]),
+    "w": st.integers(1, 1500),
+    "p": st.sampled_from([0.05, 0.3, 0.7, 1.0]),
+    "seed": st.integers(0, 2 ** 16),
+})
+
+
+@settings(max_examples=25, **SETTINGS)
+@given(c=split_case)
+def test_split_paths_property(c):
+    """Few KV heads and sequences of 9-29 key tiles: grids of a few dozen
+    row tiles, where the forward cuts full items into key chunks of 4-32
+    tiles (merged by their LSE) and the backward cuts long dQ row tiles into
+    pieces (summed in order).  The forward against the oracle and against
+    the unsplit C-ABI call (plain workspace), the backward against the
+    oracle."""
+    from switchattentionkernels_amd import _lib
+    skv = max(1, c["s"] + c["dkv"])
+    hq = c["g"] * c["hkv"]
+    gen = torch.Generator().manual_seed(c["seed"])
+    q, k, v = workloads.make_qkv(gen, c["b"], c["s"], skv, hq, c["hkv"], 128)
+    mask = torch.rand((c["b"], c["s"]), generator=gen) < c["p"]
+    do = torch.randn(q.shape, generator=gen).to(torch.bfloat16)
+    L = _lib.lib()
+    f_np, l_np = R.compact(mask.numpy())
+    plain = L.swattn_prefill_workspace_bytes(c["b"], skv, c["hkv"], 128)
+    split = L.swattn_prefill_split_workspace_bytes(c["b"], c["s"], skv, hq, c["hkv"], 128,
+                                                   c["w"], f_np.size, l_np.size)
+    tag = (f"split b{c['b']} s{c['s']} skv{skv} {hq}/{c['hkv']} w{c['w']} p{c['p']} "
+           f"seed{c['seed']} fwd split {split > plain}")
+    print(f"[property] {tag}", flush=True)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_forward(qd, kd, vd, full, local, window_size=c["w"])
+    grads = switch_gqa_prefill_backward(qd, kd, vd, o, lse, do.to(DEV), full, local,
+                                        window_size=c["w"])
+    ws = torch.empty(plain, dtype=torch.uint8, device=DEV)
+    o_u, lse_u = torch.empty_like(qd), torch.empty(q.shape[:3], dtype=torch.float32, device=DEV)
+    st_ = L.swattn_prefill_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), full.data_ptr(),
+                               full.numel(), local.data_ptr(), local.numel(), None, None, None,
+                               o_u.data_ptr(), lse_u.data_ptr(), c["b"], c["s"], skv, hq,
+                               c["hkv"], 128, c["w"], 128 ** -0.5 * oracle.LOG2E, ws.data_ptr(),
+                               plain, _lib.stream_handle(qd.device))
+    assert st_ == 0, L.swattn_last_error()
+    torch.cuda.synchronize()
+    o_ref, lse_ref = oracle.routed_attention(q, k, v, f_np, l_np, window_size=c["w"])
+    _assert_close(o, lse, o_ref, lse_ref, tag=tag)
+    _assert_close(o, lse, o_u.float().cpu(), lse_u.cpu(), tag=tag + " vs unsplit")
+    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, window_size=c["w"])
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")
