@@ -93,11 +93,11 @@ constexpr size_t kPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kPartUnits *
 // (key tile, KV head) pairs are split over their row blocks.
 constexpr int64_t kDkvTargetWgs = 512;
 constexpr int kDkvMaxSplit = 16;
-// dQ split partials: per workgroup and wave, 16 float4 units per lane (dQ^T
+// dQ piece partials: per workgroup and wave, 16 float4 units per lane (dQ^T
 // block d elements 4j .. 4j+3 in unit 4d + j), unit-major like the dK/dV ones.
 constexpr int kDqPartUnits = 16;
 constexpr size_t kDqPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kDqPartUnits * 64 * 16;   // 128 KiB
-constexpr int kDqMinTilesPerSplit = 4;   // 64-key tiles a dQ piece takes at least
+constexpr int kDqMinTilesPerPiece = 4;   // 64-key tiles a dQ piece takes at least
 // dQ LDS ring slot: K tile, V tile (16 KiB each); three slots.
 constexpr int kQStageBytes = 2 * kTileBytes;
 
@@ -419,7 +419,7 @@ __device__ __forceinline__ float4* part_unit(const BwdParams& p, int64_t wg, int
 }
 
 // Float4 unit u (= 4d + j: dQ^T block d elements 4j .. 4j+3) of (workgroup
-// wg, wave, lane) in the dQ split partials.
+// wg, wave, lane) in the dQ piece partials.
 __device__ __forceinline__ float4* dq_part_unit(const BwdParams& p, int64_t wg, int wave, int u,
                                                 int lane) {
   return reinterpret_cast<float4*>(p.dq_part) + ((wg * kBwdWaves + wave) * kDqPartUnits + u) * 64 +
@@ -995,7 +995,7 @@ inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, 
   // local one about a window).  When the longest one exceeds twice the
   // estimated tiles per workgroup slot (the sum over kDkvTargetWgs slots),
   // row tiles are cut into pieces of at most twice that many tiles (at
-  // least kDqMinTilesPerSplit), so that the longest no longer sets the
+  // least kDqMinTilesPerPiece), so that the longest no longer sets the
   // kernel's length.  (Measured on the KV-head share of a 16K-token,
   // 4-query-head prefill: pieces of 1x, 1.25x, 1.5x, 3x and 4x the
   // per-slot tiles all ran 5-15% slower than 2x, which pairs a long piece
@@ -1009,8 +1009,8 @@ inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, 
   const int64_t longest = L.items[0] > 0 ? full_len : local_len;
   L.dq_chunk = 0;
   L.dq_maxc[0] = L.dq_maxc[1] = 1;
-  if (q_items > 0 && longest > 2 * per_slot && longest > kDqMinTilesPerSplit) {
-    L.dq_chunk = std::max<int64_t>(kDqMinTilesPerSplit, 2 * per_slot);
+  if (q_items > 0 && longest > 2 * per_slot && longest > kDqMinTilesPerPiece) {
+    L.dq_chunk = std::max<int64_t>(kDqMinTilesPerPiece, 2 * per_slot);
     L.dq_maxc[0] = ceil_div(full_len, L.dq_chunk);
     L.dq_maxc[1] = ceil_div(local_len, L.dq_chunk);
   }
