@@ -92,7 +92,9 @@ def switch_gqa_prefill_backward(
     scale = ((1.0 / dim) ** 0.5 if sm_scale is None else float(sm_scale))
     if not scale > 0:
         raise ValueError("sm_scale must be positive")
-    dq = torch.zeros_like(q)
+    # The lists cover every query position once (checked above), and the
+    # kernels write every listed row (0 for a row with no key): no fill.
+    dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
     md = metadata

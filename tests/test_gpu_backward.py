@@ -278,6 +278,47 @@ def test_kv_head_share_backward():
     _grad_close(dq, rq, "kvh1 dq sampled rows", rows=torch.as_tensor(rows))
 
 
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,skv", [
+    (1, 300, 8, 2, 64, 0.3, None),      # dQ row tiles cut into pieces
+    (2, 300, 8, 2, 64, 0.3, 100),       # fewer keys than queries: rows with no key (dq = 0)
+    (1, 4096, 4, 1, 256, 0.3, None),    # pieces of 4 tiles, full and local row tiles cut
+    (1, 2000, 32, 8, 1024, 0.25, None), # no pieces
+])
+def test_backward_writes_every_dq_row(b, s, hq, hkv, w, p, skv):
+    """Through the C ABI with dq, dk and dv pre-filled with NaN: lists that
+    cover every position get every dq row written (0 for a row with no key),
+    and every dk / dv row, so the Python layer allocates them uninitialised."""
+    from switchattentionkernels_amd import _lib
+    q, k, v, do = _qkv(b * 31 + s, b, s, hq, hkv, skv)
+    m = _mask(s + 3, (b, s), p)
+    qd, kd, vd, dod = q.to(DEV), k.to(DEV), v.to(DEV), do.to(DEV)
+    full, local = build_switch_query_indices(m.to(DEV))
+    o, lse = switch_gqa_prefill_forward(qd, kd, vd, full, local, window_size=w)
+    L = _lib.lib()
+    skv_ = k.shape[1]
+    ws_bytes = L.swattn_prefill_bwd_workspace_bytes(b, skv_, hq, hkv, 128, w, full.numel(),
+                                                    local.numel())
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    dq = torch.full_like(qd, float("nan"))
+    dk = torch.full_like(kd, float("nan"))
+    dv = torch.full_like(vd, float("nan"))
+    st = L.swattn_prefill_bwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), o.data_ptr(),
+                              lse.data_ptr(), dod.data_ptr(), full.data_ptr(), full.numel(),
+                              local.data_ptr(), local.numel(), None, None, None, dq.data_ptr(),
+                              dk.data_ptr(), dv.data_ptr(), b, s, skv_, hq, hkv, 128, w,
+                              128 ** -0.5 * oracle.LOG2E, ws.data_ptr(), ws_bytes,
+                              _lib.stream_handle(qd.device))
+    assert st == 0, L.swattn_last_error()
+    torch.cuda.synchronize()
+    for name, g in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert torch.isfinite(g).all().item(), f"{name}: a row was never written"
+    rq, rk, rv = _oracle(q, k, v, do, m, w)
+    tag = f"NaN canary b{b} s{s} {hq}/{hkv} w{w} skv{skv}"
+    _grad_close(dq, rq, tag + " dq")
+    _grad_close(dk, rk, tag + " dk")
+    _grad_close(dv, rv, tag + " dv")
+
+
 def test_backward_with_no_query_rows():
     """No query rows: dq is empty and every key gets dk = dv = 0."""
     q = torch.zeros(1, 0, 4, 128, dtype=torch.bfloat16, device=DEV)
