@@ -280,7 +280,7 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *              (256-key tile, KV head) pairs also fp32 dK/dV partials of
  *              256 KiB per split workgroup (at most 256 MiB), and, when the
  *              longest dQ row tile would set that pass's length, fp32 dQ
- *              partials of 128 KiB per piece slot (at most 320 MiB);
+ *              partials of 128 KiB per piece slot (at most 192 MiB);
  *              overwritten (calls sharing it must not overlap).
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over

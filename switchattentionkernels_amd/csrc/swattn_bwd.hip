@@ -89,10 +89,13 @@ constexpr int kDkvLdsBytes = kVTileBytes + kRingSlots * kStageBytes + kInfoSlots
 // 1 KiB contiguous.
 constexpr int kPartUnits = 32;
 constexpr size_t kPartBytesPerWg = static_cast<size_t>(kBwdWaves) * kPartUnits * 64 * 16;   // 256 KiB
-// Below this many dK/dV workgroups (two per CU on a 256-CU MI355X) the
-// (key tile, KV head) pairs are split over their row blocks.
+// Below this many dK/dV workgroups (two rounds of one per CU on a 256-CU
+// MI355X: the kernel's LDS allows one) the (key tile, KV head) pairs are
+// split over their row blocks.
 constexpr int64_t kDkvTargetWgs = 512;
 constexpr int kDkvMaxSplit = 16;
+// dQ workgroups that run at once (one per CU: the 96 KiB ring allows one).
+constexpr int64_t kDqSlots = 256;
 // dQ piece partials: per workgroup and wave, 16 float4 units per lane (dQ^T
 // block d elements 4j .. 4j+3 in unit 4d + j), unit-major like the dK/dV ones.
 constexpr int kDqPartUnits = 16;
@@ -992,33 +995,33 @@ inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, 
   if (L.dkv_split > 1) o += static_cast<size_t>(pairs * L.dkv_split) * kPartBytesPerWg;
   // dQ: a row tile's key tiles, estimated per branch (a full row tile of
   // one sequence spans up to a sequence's keys, half of them on average; a
-  // local one about a window).  When the longest one exceeds twice the
-  // estimated tiles per workgroup slot (the sum over kDkvTargetWgs slots),
-  // row tiles are cut into pieces of at most twice that many tiles (at
-  // least kDqMinTilesPerPiece), so that the longest no longer sets the
-  // kernel's length.  (Measured on the KV-head share of a 16K-token,
-  // 4-query-head prefill: pieces of 1x, 1.25x, 1.5x, 3x and 4x the
-  // per-slot tiles all ran 5-15% slower than 2x, which pairs a long piece
-  // with a short row tile on a CU.)  Each row tile has room for as many
+  // local one about a window).  When the longest one exceeds the estimated
+  // tiles per workgroup slot (the sum over kDqSlots slots), row tiles are
+  // cut into pieces of at most that many tiles (at least
+  // kDqMinTilesPerPiece), so that the longest no longer sets the kernel's
+  // length.  (Measured on the KV-head share of a 16K-token, 4-query-head
+  // prefill: pieces of 0.5x, 0.625x, 0.75x, 1.5x and 2x the per-slot tiles
+  // all ran 5-15% slower than 1x.)  Each row tile has room for as many
   // pieces as its branch's longest estimate needs.
   const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
   const int64_t full_len = ceil_div(seq_kv, kBN) + 1;
   const int64_t local_len = std::min<int64_t>(full_len, ceil_div(window, kBN) + 2);
   const int64_t est = heads_kv * (L.items[0] * (full_len / 2 + 1) + L.items[1] * local_len);
-  const int64_t per_slot = ceil_div(est, kDkvTargetWgs);
+  const int64_t per_slot = ceil_div(est, kDqSlots);
   const int64_t longest = L.items[0] > 0 ? full_len : local_len;
   L.dq_chunk = 0;
   L.dq_maxc[0] = L.dq_maxc[1] = 1;
-  if (q_items > 0 && longest > 2 * per_slot && longest > kDqMinTilesPerPiece) {
-    L.dq_chunk = std::max<int64_t>(kDqMinTilesPerPiece, 2 * per_slot);
+  if (q_items > 0 && longest > per_slot && longest > kDqMinTilesPerPiece) {
+    L.dq_chunk = std::max<int64_t>(kDqMinTilesPerPiece, per_slot);
     L.dq_maxc[0] = ceil_div(full_len, L.dq_chunk);
     L.dq_maxc[1] = ceil_div(local_len, L.dq_chunk);
   }
   // Partials are indexed by the dQ workgroup; full row tiles' slots come
   // first, and local ones are only cut when their branch has more than one
-  // slot.  With the rule above fewer than 512 (row tile, KV head) pairs of a
-  // branch can be cut, each into fewer than its estimate / per_slot + 1
-  // pieces: under 1536 full and 1024 local slots, 320 MiB.
+  // slot.  With the rule above a branch can be cut only if it has fewer than
+  // 512 (full) or 256 (local) row tiles times KV heads, and their pieces
+  // number at most 512 or 256 more than that: under 1024 full and 512 local
+  // slots, 192 MiB.
   L.off_dq_nch = o;
   L.off_dq_part = o;
   if (L.dq_chunk > 0) {

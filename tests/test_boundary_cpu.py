@@ -59,25 +59,26 @@ def test_version_and_workspace():
     # tiles x 8 KV heads = 32 pairs, split min(16, 512 / 32) = 16 ways.
     # dQ: 5 full and 11 local row tiles of 256 rows, x 8 KV heads; estimated
     # key tiles 17 // 2 + 1 = 9 per full and min(17, 256 / 64 + 2) = 6 per
-    # local row tile: 8 * (5 * 9 + 11 * 6) = 888, 2 per slot of 512.  The
-    # longest (17) exceeds twice that, so row tiles are cut into pieces of
-    # max(4, 2 * 2) = 4 tiles: 5 slots per full and 2 per local row tile,
-    # 128 KiB each, after 128 int32 piece counts (512 bytes).
+    # local row tile: 8 * (5 * 9 + 11 * 6) = 888, 4 per slot of 256 (one
+    # dQ workgroup per CU).  The longest (17) exceeds that, so row tiles are
+    # cut into pieces of max(4, 4) = 4 tiles: 5 slots per full and 2 per
+    # local row tile, 128 KiB each, after 128 int32 piece counts (512
+    # bytes).
     nb = 8 * (-(-(300 * 4) // 32) + -(-(700 * 4) // 32))
     expect = (nb * 1024 + 256 + 256 + 32 * 16 * 256 * 1024 + 512
               + 8 * (5 * 5 + 11 * 2) * 128 * 1024)
     assert lib.swattn_prefill_bwd_workspace_bytes(1, 1000, 32, 8, 128, 256, 300, 700) == expect
     # config #3 (p_full 0.25 draw): 512 pairs, no dK/dV split; dQ estimate
-    # 8 * (63 * 129 + 194 * 18) = 92952, 182 per slot: the longest (257) is
-    # under twice that, no pieces
+    # 8 * (63 * 129 + 194 * 18) = 92952, 364 per slot: the longest (257) is
+    # under that, no pieces
     nb = 8 * (-(-(4028 * 4) // 32) + -(-(12356 * 4) // 32))
     expect_big = nb * 1024 + 256 + 2 * 64 * 2 * 4     # 64 key tiles x 8 KV heads = 512 pairs
     assert (lib.swattn_prefill_bwd_workspace_bytes(1, 64 * 256, 32, 8, 128, 1024, 4028, 12356)
             == expect_big)
     # its KV-head share (Hq4/Hkv1): 64 pairs split 8 ways; dQ estimate 11619,
-    # 23 per slot, pieces of 46: full row tiles get ceil(257 / 46) = 6 slots,
-    # local ones (18 tiles) one, which writes no partial, so only full slots
-    # are kept
+    # pieces of 46 tiles per slot: full row tiles get ceil(257 / 46) = 6
+    # slots, local ones (18 tiles) one, which writes no partial, so only full
+    # slots are kept
     nb = -(-(4028 * 4) // 32) + -(-(12356 * 4) // 32)
     expect_kvh1 = (nb * 1024 + 256 + 2 * 64 * 2 * 4 + 64 * 8 * 256 * 1024 + 1280
                    + 63 * 6 * 128 * 1024)
