@@ -1104,7 +1104,8 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   }
   if (L.kv_tiles_dkv * heads_kv * L.dkv_split > INT32_MAX ||
       (L.items[0] * L.dq_maxc[0] + L.items[1] * L.dq_maxc[1]) * heads_kv > INT32_MAX ||
-      (L.items[0] + L.items[1]) * heads_kv * kBwdWaves * kDqPartUnits * 64 / kThreads > INT32_MAX)
+      (L.dq_chunk > 0 &&
+       (L.items[0] + L.items[1]) * heads_kv * kBwdWaves * kDqPartUnits * 64 / kThreads > INT32_MAX))
     return invalid("swattn_prefill_bwd: grid too large");
 
   char* ws = static_cast<char*>(workspace);
