@@ -96,6 +96,29 @@ def build_probe(verbose: bool = False) -> str:
     return build(verbose=verbose, out=PROBE_LIB, sources=PROBE_SOURCES)
 
 
+C_CALLER_SRC = os.path.join(ROOT, "tests", "c_abi", "prefill_caller.cpp")
+C_CALLER = os.path.join(ROOT, "tests", "c_abi", "prefill_caller")
+
+
+def build_c_caller(verbose: bool = False) -> str:
+    """Compile the C++ test program that drives ``libswattn.so`` through the
+    C ABI alone (``tests/c_abi/prefill_caller``), with no Python or torch in
+    its process.  The program and the library then share the one HIP runtime
+    (``libamdhip64.so.7``) the loader resolves for it."""
+    cmd = [_hipcc(), "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"), C_CALLER_SRC,
+           "-L", HERE, "-Wl,-rpath," + HERE, "-lswattn"]
+    tmp = C_CALLER + ".tmp"
+    cmd += ["-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
+    os.replace(tmp, C_CALLER)
+    return C_CALLER
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
     print(build_probe(verbose=True))
+    print(build_c_caller(verbose=True))
