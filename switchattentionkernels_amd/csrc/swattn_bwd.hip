@@ -23,8 +23,8 @@
 //   operands in registers and dK^T, dV^T (128 d x 32 keys each) in
 //   accumulators; the workgroup's V rows sit in LDS.  It streams the row
 //   blocks that can see the tile (a contiguous block range per branch,
-//   found by bwd_ranges_kernel with a binary search over the monotone row
-//   bounds) through a three-slot LDS ring.  Each block's 32 Q and dO rows
+//   found by bwd_ranges_kernel with a wave-parallel search over the
+//   monotone row bounds) through a three-slot LDS ring.  Each block's 32 Q and dO rows
 //   are gathered from their positions by global_load_lds_dwordx4 (one
 //   64-bit source address per lane), from the row offsets of the block's
 //   info, which travels one block ahead through a four-slot info ring.
@@ -163,7 +163,7 @@ __device__ __forceinline__ void row_bounds(const BwdParams& p, int branch, int p
   // An empty range keeps ks = ke.  F's rule with seq_q > seq_kv + window - 1
   // gives late local rows a start past their end (and past the next
   // sequence's first start); clipped, the starts are non-decreasing along
-  // each list, as bwd_ranges_kernel's binary search needs.
+  // each list, as bwd_ranges_kernel's search needs.
   ks = min(ks, ke);
 }
 
@@ -260,39 +260,53 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
 // list, so the slots that overlap [k0, k1) are [first with end > k0, first
 // with start >= k1).
 // ---------------------------------------------------------------------------
+// The first slot in [lo, hi) of list b whose row bounds satisfy pred (false
+// ... false, true ... true along the list), or hi.  A wave searches
+// together: each step probes 64 evenly spaced slots at once and keeps the
+// gap between the last false and the first true probe, so a list of n slots
+// costs about log64(n) dependent loads instead of log2(n).  lo and hi stay
+// wave-uniform (ballot), and every probe lies in [lo, hi).
+template <bool kMeta, class Pred>
+__device__ int wave_lower_bound(const BwdParams& p, int b, int lo, int hi, Pred pred) {
+  const int lane = threadIdx.x & 63;
+  while (lo < hi) {
+    const int64_t span = hi - lo;
+    const int probe = lo + static_cast<int>(span * lane / 64);
+    const int pm = p.idx[b][probe];
+    int ks, ke;
+    row_bounds<kMeta>(p, b, pos_ok(p, pm) ? pm : 0, ks, ke);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(pred(ks, ke));
+    if (m == 0) {
+      lo += static_cast<int>(span * 63 / 64) + 1;   // past the last probe
+    } else {
+      const int first = __builtin_ctzll(m);
+      hi = lo + static_cast<int>(span * first / 64);
+      if (first > 0) lo += static_cast<int>(span * (first - 1) / 64) + 1;
+    }
+  }
+  return lo;
+}
+
+// One wave per (branch, key tile).
 template <bool kMeta>
 __global__ __launch_bounds__(kThreads) void bwd_ranges_kernel(const BwdParams p) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= 2 * p.kv_tiles_dkv) return;
+  const int i = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  if (i >= 2 * p.kv_tiles_dkv) return;   // whole waves
   const int b = i / p.kv_tiles_dkv, t = i - b * p.kv_tiles_dkv;
   const int k0 = t * kKeysDkv, k1 = min(k0 + kKeysDkv, p.total_kv);
   const int n = p.count[b];
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    int ks, ke;
-    const int pm = p.idx[b][mid];
-    row_bounds<kMeta>(p, b, pos_ok(p, pm) ? pm : 0, ks, ke);
-    if (ke > k0) hi = mid; else lo = mid + 1;
-  }
-  const int s_lo = lo;
-  hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    int ks, ke;
-    const int pm = p.idx[b][mid];
-    row_bounds<kMeta>(p, b, pos_ok(p, pm) ? pm : 0, ks, ke);
-    if (ks >= k1) hi = mid; else lo = mid + 1;
-  }
-  const int s_hi = lo;
+  const int s_lo = wave_lower_bound<kMeta>(p, b, 0, n, [=](int, int ke) { return ke > k0; });
+  const int s_hi = wave_lower_bound<kMeta>(p, b, s_lo, n, [=](int ks, int) { return ks >= k1; });
   int blo = 0, bhi = 0;
   if (s_lo < s_hi) {
     const int64_t G = p.group;
     blo = static_cast<int>((s_lo * G) / kBRows);
     bhi = static_cast<int>((s_hi * G + kBRows - 1) / kBRows);
   }
-  p.ranges[2 * i] = blo;
-  p.ranges[2 * i + 1] = bhi;
+  if ((threadIdx.x & 63) == 0) {
+    p.ranges[2 * i] = blo;
+    p.ranges[2 * i + 1] = bhi;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1158,7 +1172,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   p.scale = scale_log2 * 0.69314718055994531f;   // sm_scale = c * ln 2
 
   const hipStream_t st = as_stream(stream);
-  const uint32_t rgrid = static_cast<uint32_t>(ceil_div(2 * L.kv_tiles_dkv, kThreads));
+  const uint32_t rgrid = static_cast<uint32_t>(ceil_div(2 * L.kv_tiles_dkv, kThreads / 64));
   if (meta)
     hipLaunchKernelGGL(bwd_ranges_kernel<true>, dim3(rgrid), dim3(kThreads), 0, st, p);
   else
