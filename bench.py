@@ -1,6 +1,6 @@
 """Benchmark: routed GQA prefill on one MI355X.
 
-Metric (BASELINE.json): routed-attention TFLOP/s and ms per prefill at
+Metric: routed-attention TFLOP/s and ms per prefill at
 S=16k Hq32/Hkv8, plus the fraction of bf16 MFMA peak.
 
 Workload (the config the metric is quoted on): B=1, S=16384, Hq=32, Hkv=8,

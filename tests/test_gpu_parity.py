@@ -1,6 +1,6 @@
 """GPU parity: libswattn.so (through the public API and the C ABI) vs the CPU oracle.
 
-Bars:
+Bars (the target's stated tolerances):
 * compaction index lists: bit-exact (torch.equal);
 * O: max-abs <= 2e-2 and mean-abs <= 2e-3 against the fp32 oracle (bf16 output);
 * LSE (log2): |delta| <= 1e-3 * max(1, |ref|)  (relative 1e-3 with an absolute
