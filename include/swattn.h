@@ -7,7 +7,8 @@
  * that stream and returns without synchronising.  Nothing here allocates
  * device memory: scratch space is passed in by the caller.  bf16 row tensors
  * (q, k, v, out and their gradients, KV caches, merge partials) must be
- * 16-byte aligned; a misaligned one is rejected with SWATTN_EINVAL.
+ * 16-byte aligned, and workspaces 256-byte aligned (as hipMalloc returns);
+ * a misaligned one is rejected with SWATTN_EINVAL.
  *
  * Return value: SWATTN_OK (0) on success, a negative SWATTN_E* code for an
  * invalid argument detected on the host, or a positive hipError_t from the

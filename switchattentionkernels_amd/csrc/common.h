@@ -34,6 +34,9 @@ inline int invalid(const std::string& msg) {
 // in 16-byte pieces, by vector loads and global -> LDS DMAs: their base
 // pointers must be 16-byte aligned.
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Workspaces hold float4 / int64 records at 256-byte-aligned offsets from
+// their start, which must itself be 256-byte aligned (as hipMalloc returns).
+inline bool aligned256(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 255u) == 0; }
 
 // popcount(mask & lanes_below_me) without a lane-mask table.
 __device__ __forceinline__ int count_below(uint64_t mask) {

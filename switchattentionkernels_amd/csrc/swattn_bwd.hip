@@ -1116,6 +1116,7 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
     set_error("swattn_prefill_bwd: workspace smaller than swattn_prefill_bwd_workspace_bytes()");
     return SWATTN_EWORKSPACE;
   }
+  if (!aligned256(workspace)) return invalid("swattn_prefill_bwd: workspace must be 256-byte aligned");
   if (L.kv_tiles_dkv * heads_kv * L.dkv_split > INT32_MAX ||
       (L.items[0] * L.dq_maxc[0] + L.items[1] * L.dq_maxc[1]) * heads_kv > INT32_MAX ||
       (L.dq_chunk > 0 &&

@@ -540,6 +540,7 @@ int swattn_decode_fwd(const void* q, const void* k_cache, const void* v_cache,
     set_error("swattn_decode_fwd: workspace smaller than swattn_decode_workspace_bytes()");
     return SWATTN_EWORKSPACE;
   }
+  if (!aligned256(workspace)) return invalid("swattn_decode_fwd: workspace must be 256-byte aligned");
   return decode_launch(name, q, k_cache, v_cache, cache_lens, full, out, lse, batch, cache_len,
                        heads_q, heads_kv, window, scale_log2, static_cast<char*>(workspace),
                        stream);

@@ -782,6 +782,7 @@ extern "C" int swattn_prefill_fwd(const void* q, const void* k, const void* v,
     set_error("swattn_prefill_fwd: workspace smaller than swattn_prefill_workspace_bytes()");
     return SWATTN_EWORKSPACE;
   }
+  if (!aligned256(workspace)) return invalid("swattn_prefill_fwd: workspace must be 256-byte aligned");
 
   FwdParams p{};
   p.q = static_cast<const uint16_t*>(q);

@@ -345,6 +345,7 @@ int compact_impl(const Src& src, bool src_null, int64_t n, int32_t* indices, int
       set_error(std::string(name) + ": workspace too small");
       return SWATTN_EWORKSPACE;
     }
+    if (!aligned256(workspace)) return invalid(std::string(name) + ": workspace must be 256-byte aligned");
     int32_t* bc = static_cast<int32_t*>(workspace);
     hipLaunchKernelGGL(compact_count_kernel<Src>, dim3(nb), dim3(kCompactThreads), 0, st, src, n,
                        bc);

@@ -109,6 +109,20 @@ CHILD = textwrap.dedent('''
     parts = (ctypes.c_void_p * 2)(P, P)
     unaligned(L.swattn_merge_partials(parts, lses, 2, M, P, 10, 128, None),
               "swattn_merge_partials")
+    # workspaces must be 256-byte aligned
+    W = P + 16
+    def ws_unaligned(rc, name):
+        err(rc, EINVAL, name)
+        assert b"256-byte aligned" in L.swattn_last_error(), L.swattn_last_error()
+    ws_unaligned(L.swattn_prefill_fwd(P, P, P, P, 100, P, 100, None, None, None, P, P, 1, 200,
+                                      200, 32, 8, 128, 64, 0.1, W, 1 << 30, None),
+                 "swattn_prefill_fwd")
+    ws_unaligned(L.swattn_prefill_bwd(P, P, P, P, P, P, P, 100, P, 100, None, None, None, P, P,
+                                      P, 1, 200, 200, 32, 8, 128, 64, 0.1, W, wsb, None),
+                 "swattn_prefill_bwd")
+    ws_unaligned(L.swattn_decode_fwd(P, P, P, P, P, P, P, 4, 100, 8, 2, 128, 64, 0.1, W, 1 << 30,
+                                     None), "swattn_decode_fwd")
+    ws_unaligned(L.swattn_compact(P, 100000, P, P, W, 1 << 20, None), "swattn_compact")
     print("host checks ok")
 ''')
 
