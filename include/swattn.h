@@ -282,10 +282,13 @@ int swattn_decode_fwd_noalloc(const void* q, const void* k_cache, const void* v_
  *              256 KiB per split workgroup (at most 256 MiB), and, when the
  *              longest dQ row tile would set that pass's length, fp32 dQ
  *              partials of 128 KiB per piece slot (at most 192 MiB);
- *              overwritten (calls sharing it must not overlap).
+ *              overwritten (calls sharing it must not overlap).  The
+ *              query takes the call's window to estimate the local rows'
+ *              key ranges; pass the same shapes, window and list lengths
+ *              to both.
  * Each list's key bounds must be non-decreasing along the list (true for
  * F:145-155 and for swattn_build_metadata / swattn_shard_bounds over
- * ascending positions): the keys a row block can see are found by binary
+ * ascending positions): the keys a row block can see are found by a
  * search over them.
  */
 size_t swattn_prefill_bwd_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t heads_q,
