@@ -319,6 +319,21 @@ def test_backward_writes_every_dq_row(b, s, hq, hkv, w, p, skv):
     _grad_close(dv, rv, tag + " dv")
 
 
+@pytest.mark.parametrize("qk_scale", [4.0, 0.05])
+def test_backward_peaked_and_flat_softmax(qk_scale):
+    """Gradients when rows are nearly one-hot (Q, K x4) or nearly uniform
+    (Q, K x0.05), against the oracle."""
+    q, k, v, do = _qkv(23, 1, 600, 8, 2)
+    q, k = (q.float() * qk_scale).to(torch.bfloat16), (k.float() * qk_scale).to(torch.bfloat16)
+    m = _mask(23, (1, 600), 0.4)
+    dq, dk, dv = _run(q, k, v, do, m, 150)
+    rq, rk, rv = _oracle(q, k, v, do, m, 150)
+    tag = f"q,k x{qk_scale}"
+    _grad_close(dq, rq, tag + " dq")
+    _grad_close(dk, rk, tag + " dk")
+    _grad_close(dv, rv, tag + " dv")
+
+
 def test_backward_with_no_query_rows():
     """No query rows: dq is empty and every key gets dk = dv = 0."""
     q = torch.zeros(1, 0, 4, 128, dtype=torch.bfloat16, device=DEV)

@@ -321,6 +321,21 @@ def test_forward_custom_scale():
     _assert_close(o, lse, o_ref, lse_ref, tag="sm_scale=0.02")
 
 
+@pytest.mark.parametrize("qk_scale,sm_scale", [(4.0, None), (1.0, 1.0), (0.05, None)])
+def test_forward_peaked_and_flat_softmax(qk_scale, sm_scale):
+    """Score ranges far from the N(0,1) default: Q and K scaled by 4 (or the
+    softmax scale raised to 1), so that rows are nearly one-hot and the
+    running maximum moves often (the lazy rescale fires), and Q, K scaled by
+    0.05, so that rows are nearly uniform.  Same bars against the oracle."""
+    gen = torch.Generator().manual_seed(21)
+    q, k, v = workloads.make_qkv(gen, 1, 700, 700, 8, 2, 128)
+    q, k = (q.float() * qk_scale).to(torch.bfloat16), (k.float() * qk_scale).to(torch.bfloat16)
+    m = _mask(21, (1, 700), 0.4)
+    o, lse, _, _ = _gpu_run(q, k, v, m, 200, sm_scale=sm_scale)
+    o_ref, lse_ref = _oracle(q, k, v, m, 200, sm_scale=sm_scale)
+    _assert_close(o, lse, o_ref, lse_ref, tag=f"q,k x{qk_scale} sm_scale {sm_scale}")
+
+
 def test_cpu_config_every_row():
     wl = workloads.build("cpu", seed=0)
     o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], wl["mask"], wl["window"])
