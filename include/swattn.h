@@ -132,7 +132,7 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
  * query tile and head (V:402-445).  When the longest full item (a causal row
  * tile late in a sequence) is long against the rest of the work, as with few
  * KV heads (one GPU's share of a KV-head split) or short sequences on few
- * heads, a workgroup per chunk of 4 to 32 key tiles (planned from the shape)
+ * heads, a workgroup per chunk of 4 to 64 key tiles (planned from the shape)
  * and a merge of the chunks by their log2 LSE (V:236-241) keep it from
  * setting the kernel's length.  Returns swattn_prefill_workspace_bytes() when
  * no split would run, a larger size (fp32 partial rows of the split items)

@@ -85,7 +85,7 @@ def test_version_and_workspace():
     assert (lib.swattn_prefill_bwd_workspace_bytes(1, 16384, 4, 1, 128, 1024, 4028, 12356)
             == expect_kvh1)
     # key-range split of the forward: one GPU's share of config #3 split by KV
-    # head (Hq4/Hkv1) takes it (chunks of 32 tiles, 9 slots per full item),
+    # head (Hq4/Hkv1) takes it (chunks of 64 tiles, 5 slots per full item),
     # config #3 itself does not
     base = lib.swattn_prefill_workspace_bytes(1, 16384, 1, 128)
     big = lib.swattn_prefill_split_workspace_bytes(1, 16384, 16384, 4, 1, 128, 1024, 4028, 12356)
@@ -96,7 +96,8 @@ def test_version_and_workspace():
     # config #1 (8 full and 24 local items of 128 rows, 2 KV heads): estimate
     # 2 * (8 * (16 // 2 + 2) + 24 * (256 / 64 + 2)) = 448 tiles, 0 per slot of
     # 512, so chunks of the minimum 4 tiles; the longest item (17 tiles) spans
-    # two or more, and each full item gets ceil(16 / 4) + 1 = 5 slots.  After
+    # more than one and a half, and each full item gets ceil(16 / 4) + 1 = 5
+    # slots.  After
     # the V^T tiles (2 x 16 tiles x 16 KiB): fp32 O rows (128 x 128) and LSE
     # (128) per slot, one int2 per full item, each part 256-byte aligned.
     slots = 8 * 2 * 5
