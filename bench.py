@@ -29,10 +29,12 @@ The JSON line also carries:
   whole config #1 prefill (median of 10 after 2 warm-ups);
 * comparators: the same kernel on all-full routing (dense causal), torch
   SDPA causal (flash backend) on the same shape, the compaction alone, the
-  routed decode extension (64 sequences, 8192-key caches) against HBM, and
-  the routed backward (dq, dk, dv) of the same prefill.
+  routed decode extension (64 sequences, 8192-key caches) against HBM, the
+  routed backward (dq, dk, dv) of the same prefill, and one GPU's share of
+  the configuration under a KV-head split (Hq4/Hkv1), forward and
+  backward, with the fraction of linear scaling 8 such GPUs would give.
 
-``--configs cpu,b2,s16k,varlen,s64k`` instead times the forward and the
+``--configs cpu,b2,s16k,varlen,s64k,kvh1`` instead times the forward and the
 backward on each named workload (one JSON line each, no roofline);
 ``--p-sweep 0,0.1,0.25,0.5,1`` times config #3's attention call at each
 router density, beside the dense-causal call (one JSON line each).
@@ -475,6 +477,33 @@ def main():
     except Exception as exc:  # comparator only
         print(f"[bench] backward comparator unavailable: {exc}", file=sys.stderr, flush=True)
 
+    # ---- one GPU's share under a KV-head split (the sharding design) -------------
+    # Hkv / 8 KV heads with their query heads: what each of 8 GPUs would run,
+    # timed on this one, forward and backward; "linear" is 8 x that share's
+    # time against the whole configuration's on one GPU.
+    kv_share = None
+    try:
+        from switchattentionkernels_amd import switch_gqa_prefill_backward
+        wl_s = workloads.build("kvh1", seed=args.seed)
+        qs, ks, vs, ms = (wl_s[x].to(dev) for x in ("q", "k", "v", "mask"))
+        fs, ls = build_switch_query_indices(ms)
+        f_share = settled_ms(lambda: switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=W))
+        o_s, lse_s = switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=W)
+        do_s = torch.randn(qs.shape, generator=torch.Generator().manual_seed(args.seed + 2))
+        do_s = do_s.to(torch.bfloat16).to(dev)
+        b_share = settled_ms(lambda: switch_gqa_prefill_backward(qs, ks, vs, o_s, lse_s, do_s, fs,
+                                                                 ls, window_size=W))
+        kv_share = {"workload": f"kvh1: B1 S{qs.shape[1]} Hq{qs.shape[2]}/Hkv{ks.shape[2]} W{W}, "
+                                f"Bernoulli(0.25), seed {args.seed}",
+                    "fwd_ms": round(f_share, 4),
+                    "fwd_linear_frac": round(attn_ms / (8 * f_share), 3),
+                    "bwd_ms": round(b_share, 4),
+                    "bwd_linear_frac": None if backward is None
+                    else round(backward["ms"] / (8 * b_share), 3)}
+        del qs, ks, vs, ms, fs, ls, o_s, lse_s, do_s
+    except Exception as exc:  # comparator only
+        print(f"[bench] KV-head share comparator unavailable: {exc}", file=sys.stderr, flush=True)
+
     # ---- traffic: copied from the committed rocprofv3 --pmc summary, if any ------
     # (byte counters cannot be read inside this timed run; the file states the
     # command and the calibration that produced the figure)
@@ -588,6 +617,7 @@ def main():
             "merge_hbm_gbs": round(merge_bytes / (merge_ms * 1e-3) / 1e9, 1),
             "decode": decode,
             "backward": backward,
+            "kv_head_share": kv_share,
         },
     }
     print(json.dumps(res), flush=True)
