@@ -370,10 +370,18 @@ def main():
         return
 
     # ---- attention kernel alone (roofline) -------------------------------------
-    # Timed first: its launches also bring the chip from idle to the clock it
-    # holds under this load, which a few warm-up steps alone do not (20 steps
-    # after 5 warm-ups measured about 10 % slower per step than 200 after 50).
-    attn_ms = time_launches(lambda: attn(full, local), max(args.steps, 50), warmup=10)
+    # Timed first, after about 0.4 s of untimed calls: they bring the chip from
+    # idle to the clock it holds under this load (200 calls after only 10
+    # warm-ups measured 1.4 % slower than after the clock settled), and they
+    # leave it there for the timed steps below.
+    attn(full, local)
+    torch.cuda.synchronize()
+    t_one = time.perf_counter()
+    attn(full, local)
+    torch.cuda.synchronize()
+    attn_warm = max(10, int(0.4 / max(time.perf_counter() - t_one, 1e-5)))
+    attn_calls = max(args.steps, 50)
+    attn_ms = time_launches(lambda: attn(full, local), attn_calls, warmup=attn_warm)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
 
     # ---- timed region: K full steps -------------------------------------------
@@ -589,8 +597,9 @@ def main():
                      "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false, false>",
                      "kernel_ms": round(attn_ms, 4),
                      "kernel_timing": f"HIP events on the launch stream around "
-                                      f"{max(args.steps, 50)} back-to-back calls after 10 "
-                                      f"warm-ups, in this run",
+                                      f"{attn_calls} back-to-back calls after {attn_warm} "
+                                      f"untimed calls (about 0.4 s: clock settled), in this "
+                                      f"run",
                      "gather_scatter": {
                          "bytes": gather_scatter_bytes,
                          "what": "Q rows read and O / LSE rows written at their listed "
