@@ -135,8 +135,8 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
  * heads, a workgroup per chunk of 4 to 64 key tiles (planned from the shape)
  * and a merge of the chunks by their log2 LSE (V:236-241) keep it from
  * setting the kernel's length.  Returns swattn_prefill_workspace_bytes() when
- * no split would run, a larger size (fp32 partial rows of the split items)
- * when it would, 0 for an unsupported shape.  The forward splits only if it
+ * no split would run, a larger size (fp32 partial rows of the split items,
+ * at most 200 MiB more) when it would, 0 for an unsupported shape.  The forward splits only if it
  * receives at least this much workspace; with less it runs unsplit.  Rows of
  * items that lie inside one chunk are computed exactly as without a split.
  */

@@ -693,6 +693,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // the chunks' fp32 O rows, their LSE and one (chunks, first chunk) per full
 // item.
 constexpr int64_t kSplitSlots = 512;
+constexpr int64_t kSplitMaxChunks = 2048;
 struct SplitPlan {
   int32_t maxc = 1;
   int32_t tiles = kSplitTiles;
@@ -710,7 +711,12 @@ inline SplitPlan split_plan(int32_t batch, int64_t seq_kv, int32_t heads_q, int3
   const int64_t local_tiles = ceil_div(std::min<int64_t>(window, seq_kv), kBN) + 2;
   const int64_t est = heads_kv * (full_items * (seq_tiles / 2 + 2) + local_items * local_tiles);
   const int64_t per_slot = est / kSplitSlots;
-  const int64_t chunk = std::min<int64_t>(kSplitTiles, std::max<int64_t>(kSplitMinTiles, (3 * per_slot) / 2));
+  int64_t chunk = std::min<int64_t>(kSplitTiles, std::max<int64_t>(kSplitMinTiles, (3 * per_slot) / 2));
+  // Very long sequences: chunks long enough that the chunk slots number at
+  // most about kSplitMaxChunks.  With the split condition below, full items
+  // times KV heads stay under 512, so the slots stay under kSplitMaxChunks +
+  // 1024 and their fp32 rows under 200 MiB.
+  chunk = std::max<int64_t>(chunk, ceil_div(full_items * heads_kv * seq_tiles, kSplitMaxChunks));
   if (2 * longest <= 3 * chunk || longest <= 2 * per_slot) return sp;
   sp.tiles = static_cast<int32_t>(chunk);
   sp.maxc = static_cast<int32_t>(ceil_div(seq_tiles, chunk) + 1);

@@ -197,3 +197,42 @@ def test_workloads_are_seeded_and_shaped():
     assert rp[:20000].float().mean() < rp[-20000:].float().mean()
     vl = workloads.varlen_lengths(torch.Generator().manual_seed(1))
     assert len(vl) == 8 and all(512 <= x <= 8192 for x in vl)
+
+
+def test_workspace_partials_stay_within_their_stated_bounds():
+    """The workspace queries over many shapes (no GPU needed): the backward's
+    dK/dV partials stay within 256 MiB and its dQ partials within 192 MiB
+    beyond the row-info blocks, and the forward's split workspace exceeds the
+    plain one by at most 200 MiB, as include/swattn.h states."""
+    from hypothesis import given, settings, strategies as st
+
+    lib = _lib.lib()
+    MiB = 1 << 20
+
+    @settings(max_examples=300, deadline=None, derandomize=True, database=None)
+    @given(b=st.integers(1, 8), skv=st.integers(1, 1 << 17), hkv=st.integers(1, 16),
+           g=st.sampled_from([1, 2, 4, 5, 8]), w=st.integers(1, 1 << 16),
+           frac_full=st.floats(0.0, 1.0), frac_rows=st.floats(0.0, 1.0))
+    def check(b, skv, hkv, g, w, frac_full, frac_rows):
+        hq = hkv * g
+        n = int(b * skv * frac_rows)
+        nf = int(n * frac_full)
+        nl = n - nf
+        bwd = lib.swattn_prefill_bwd_workspace_bytes(b, skv, hq, hkv, 128, w, nf, nl)
+        assert bwd > 0
+        blocks = hkv * (-(-nf * g // 32) + -(-nl * g // 32))
+        kv_tiles = -(-(b * skv) // 256)
+        q_items = hkv * (-(-nf * g // 256) + -(-nl * g // 256))
+        base = blocks * 1024 + 256 + (2 * kv_tiles * 2 * 4 + 255) // 256 * 256
+        extra = bwd - base
+        assert 0 <= extra <= 256 * MiB + 192 * MiB + (q_items * 4 + 255) // 256 * 256, \
+            (b, skv, hq, hkv, w, nf, nl, bwd, base)
+        plain = lib.swattn_prefill_workspace_bytes(b, skv, hkv, 128)
+        split = lib.swattn_prefill_split_workspace_bytes(b, skv, skv, hq, hkv, 128, w, nf, nl)
+        assert plain <= split <= plain + 200 * MiB, (b, skv, hq, hkv, w, nf, nl, split - plain)
+
+    check()
+    # a long sequence with few listed rows: chunk slots bounded by lengthening the chunks
+    plain = lib.swattn_prefill_workspace_bytes(1, 129435, 4, 128)
+    split = lib.swattn_prefill_split_workspace_bytes(1, 129435, 129435, 16, 4, 128, 10682, 2807, 357)
+    assert plain < split <= plain + 200 * MiB

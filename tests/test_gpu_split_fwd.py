@@ -159,3 +159,26 @@ def test_kv_head_share_of_s16k():
     rows = np.unique(np.concatenate([rng.integers(0, 16384, 200), f_np[-48:]]))
     o_r, l_r = oracle.routed_attention(q, k, v, f_np, l_np, window_size=wl["window"], rows=rows)
     _assert_close(o, lse, o_r, l_r, rows=rows, tag="kvh1 vs oracle")
+
+
+def test_long_sparse_sequence_lengthens_the_chunks():
+    """A 131072-key sequence with 2 % full rows (one KV head): chunks of 64
+    tiles would need 33 slots per full item, so the plan lengthens them
+    (about 2048 chunk slots in all) and the split workspace stays small.
+    Sampled rows, late full rows included, against the oracle; no row left
+    unwritten."""
+    b, s, hq, hkv, w = 1, 131072, 4, 1, 1024
+    gen = torch.Generator().manual_seed(41)
+    q, k, v = workloads.make_qkv(gen, b, s, s, hq, hkv, 128)
+    mask = torch.rand((b, s), generator=gen) < 0.02
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse, base, big = _abi_forward(qd, kd, vd, full, local, w, split=True)
+    assert base < big <= base + (200 << 20)
+    print(f"long sparse: workspace {base} -> {big}", flush=True)
+    assert not torch.isnan(o).any() and not torch.isnan(lse).any()
+    f_np, l_np = R.compact(mask.numpy())
+    rng = np.random.default_rng(41)
+    rows = np.unique(np.concatenate([rng.integers(0, s, 100), f_np[-24:], f_np[:4]]))
+    o_r, l_r = oracle.routed_attention(q, k, v, f_np, l_np, window_size=w, rows=rows)
+    _assert_close(o, lse, o_r, l_r, rows=rows, tag="long sparse vs oracle")
