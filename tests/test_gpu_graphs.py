@@ -6,7 +6,9 @@ index lists that need no device check) can be captured once and replayed.  Each 
 several times with new inputs written eagerly between replays, and every
 replay must equal an eager call on the same inputs bit for bit.  The decode
 replays also change the cache lengths and routing: its work split is planned
-on the device at each replay, not baked into the graph.
+on the device at each replay, not baked into the graph.  The prefill shapes
+are small grids, so the graphs also hold the forward's key-range split and
+merge, the backward's dK/dV split and dQ pieces, and their reduce kernels.
 """
 
 import pytest
