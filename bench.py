@@ -494,14 +494,15 @@ def main():
         from switchattentionkernels_amd import switch_gqa_prefill_backward
         wl_s = workloads.build("kvh1", seed=args.seed)
         qs, ks, vs, ms = (wl_s[x].to(dev) for x in ("q", "k", "v", "mask"))
+        ws_ = wl_s["window"]
         fs, ls = build_switch_query_indices(ms)
-        f_share = settled_ms(lambda: switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=W))
-        o_s, lse_s = switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=W)
+        f_share = settled_ms(lambda: switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=ws_))
+        o_s, lse_s = switch_gqa_prefill_forward(qs, ks, vs, fs, ls, window_size=ws_)
         do_s = torch.randn(qs.shape, generator=torch.Generator().manual_seed(args.seed + 2))
         do_s = do_s.to(torch.bfloat16).to(dev)
         b_share = settled_ms(lambda: switch_gqa_prefill_backward(qs, ks, vs, o_s, lse_s, do_s, fs,
-                                                                 ls, window_size=W))
-        kv_share = {"workload": f"kvh1: B1 S{qs.shape[1]} Hq{qs.shape[2]}/Hkv{ks.shape[2]} W{W}, "
+                                                                 ls, window_size=ws_))
+        kv_share = {"workload": f"kvh1: B1 S{qs.shape[1]} Hq{qs.shape[2]}/Hkv{ks.shape[2]} W{ws_}, "
                                 f"Bernoulli(0.25), seed {args.seed}",
                     "fwd_ms": round(f_share, 4),
                     "fwd_linear_frac": round(attn_ms / (8 * f_share), 3),
