@@ -488,10 +488,18 @@ def main():
     # ---- one GPU's share under a KV-head split (the sharding design) -------------
     # Hkv / 8 KV heads with their query heads: what each of 8 GPUs would run,
     # timed on this one, forward and backward; "linear" is 8 x that share's
-    # time against the whole configuration's on one GPU.
+    # time against the whole configuration's on one GPU, both sides timed
+    # alike: the public API call, settled.
     kv_share = None
     try:
         from switchattentionkernels_amd import switch_gqa_prefill_backward
+        f_whole = settled_ms(lambda: switch_gqa_prefill_forward(q, k, v, full, local, window_size=W))
+        o_w, lse_w = switch_gqa_prefill_forward(q, k, v, full, local, window_size=W)
+        do_w = torch.randn(q.shape, generator=torch.Generator().manual_seed(args.seed + 1))
+        do_w = do_w.to(torch.bfloat16).to(dev)
+        b_whole = settled_ms(lambda: switch_gqa_prefill_backward(q, k, v, o_w, lse_w, do_w, full,
+                                                                 local, window_size=W))
+        del o_w, lse_w, do_w
         wl_s = workloads.build("kvh1", seed=args.seed)
         qs, ks, vs, ms = (wl_s[x].to(dev) for x in ("q", "k", "v", "mask"))
         ws_ = wl_s["window"]
@@ -505,10 +513,11 @@ def main():
         kv_share = {"workload": f"kvh1: B1 S{qs.shape[1]} Hq{qs.shape[2]}/Hkv{ks.shape[2]} W{ws_}, "
                                 f"Bernoulli(0.25), seed {args.seed}",
                     "fwd_ms": round(f_share, 4),
-                    "fwd_linear_frac": round(attn_ms / (8 * f_share), 3),
+                    "whole_fwd_ms": round(f_whole, 4),
+                    "fwd_linear_frac": round(f_whole / (8 * f_share), 3),
                     "bwd_ms": round(b_share, 4),
-                    "bwd_linear_frac": None if backward is None
-                    else round(backward["ms"] / (8 * b_share), 3)}
+                    "whole_bwd_ms": round(b_whole, 4),
+                    "bwd_linear_frac": round(b_whole / (8 * b_share), 3)}
         del qs, ks, vs, ms, fs, ls, o_s, lse_s, do_s
     except Exception as exc:  # comparator only
         print(f"[bench] KV-head share comparator unavailable: {exc}", file=sys.stderr, flush=True)

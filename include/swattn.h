@@ -39,7 +39,10 @@ extern "C" {
 #define SWATTN_ERR_LOCAL_ORDER 8  /* V:301-302, local list                                    */
 #define SWATTN_ERR_OVERLAP 16     /* a position in both lists (contract of V:341-342)         */
 
-/* Library version, (major << 16) | minor. */
+/* Library version, (major << 16) | minor.  0.2 changed the signature of
+ * swattn_prefill_bwd_workspace_bytes (a window argument before n_full) and
+ * took the MFMA-rate probe out of this library; callers built against 0.1
+ * must be rebuilt. */
 int swattn_version(void);
 
 /* Message for the last non-zero status returned on the calling thread. */
@@ -132,8 +135,10 @@ size_t swattn_prefill_workspace_bytes(int32_t batch, int64_t seq_kv, int32_t hea
  * query tile and head (V:402-445).  When the longest full item (a causal row
  * tile late in a sequence) is long against the rest of the work, as with few
  * KV heads (one GPU's share of a KV-head split) or short sequences on few
- * heads, a workgroup per chunk of 4 to 64 key tiles (planned from the shape)
- * and a merge of the chunks by their log2 LSE (V:236-241) keep it from
+ * heads, a workgroup per chunk of key tiles (planned from the shape: 4 to 64
+ * tiles, longer for very long sequences so that the chunk slots number at
+ * most about 2048) and a merge of the chunks by their log2 LSE (V:236-241)
+ * keep it from
  * setting the kernel's length.  Returns swattn_prefill_workspace_bytes() when
  * no split would run, a larger size (fp32 partial rows of the split items,
  * at most 200 MiB more) when it would, 0 for an unsupported shape.  The forward splits only if it

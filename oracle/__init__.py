@@ -44,7 +44,12 @@ Pinning (how each function is checked, see ``tests/test_oracle.py``)
                            pure-Python brute force, which shares no code with
                            it; sum_j dk_j = 0 and sum_j dv_j = sum_i dO_i per
                            KV head (softmax shift invariance, rows of P sum
-                           to one).
+                           to one).  With ``out`` (Delta = dO . out, the
+                           FlashAttention-2 convention): == the exact
+                           gradient for out = O; for a rounded out, dq moves
+                           by exactly ``-scale * (dO . (out - O)) * P k`` per
+                           row (``delta_shift_bound``), and a dropped or
+                           doubled Delta breaks that bound.
 
 Parity of the exact bf16 bits produced by the reference's TileLang kernels is
 unpinned (those kernels need TileLang + Hopper, neither exists here); the
@@ -71,5 +76,6 @@ from .attention import (  # noqa: F401
     merge_partials,
     decode_attention,
     routed_attention_backward,
+    delta_shift_bound,
     LOG2E,
 )

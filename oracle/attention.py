@@ -231,14 +231,36 @@ def decode_attention(q, k_cache, v_cache, cache_lens, full_mask, *, window_size=
     return out, lse
 
 
-def _score_grad(p, dp):
-    """dS = P * (dP - rowsum(P * dP)): the softmax Jacobian applied to dP."""
-    return p * (dp - (p * dp).sum(-1, keepdim=True))
+def _score_grad(p, dp, delta=None):
+    """dS = P * (dP - Delta): the softmax Jacobian applied to dP, with
+    Delta = rowsum(P * dP) unless a per-row Delta is given."""
+    if delta is None:
+        delta = (p * dp).sum(-1, keepdim=True)
+    return p * (dp - delta)
+
+
+def delta_shift_bound(out_used, out_exact, grad_out, pk, scale):
+    """Per-row size of the dq change that the FlashAttention-2 Delta brings.
+
+    A backward that takes ``Delta_r = dO_r . out_r`` from a rounded forward
+    output ``out`` instead of the exact ``dO_r . O_r`` computes, in exact
+    arithmetic otherwise, ``dq_r - scale * delta_r * sum_j P_rj k_j`` with
+    ``delta_r = dO_r . (out_r - O_r)`` (see ``routed_attention_backward``).
+    Returns ``scale * |delta_r| * ||sum_j P_rj k_j||_2`` per flattened row
+    and query head, ``[T, Hq]`` in float64, from the forward output the
+    backward used, the exact one, ``dO`` and the ``"pk"`` term that
+    ``routed_attention_backward(..., delta_terms=...)`` records.
+    """
+    hq, d = int(grad_out.shape[-2]), int(grad_out.shape[-1])
+    do = grad_out.reshape(-1, hq, d).double()
+    diff = out_used.reshape(-1, hq, d).double() - out_exact.reshape(-1, hq, d).double()
+    delta = (do * diff).sum(-1)
+    return float(scale) * delta.abs() * pk.reshape(-1, hq, d).double().norm(dim=-1)
 
 
 def routed_attention_backward(q, k, v, grad_out, full_idx, local_idx, *, window_size=1024,
                               metadata=None, sm_scale=None, chunk=256, dtype=torch.float32,
-                              rows=None):
+                              rows=None, out=None, delta_terms=None):
     """Gradients of the routed attention output, dense and masked, in ``dtype``.
 
     The reference is forward-only (V:14-15); this is the derivative of the
@@ -249,6 +271,18 @@ def routed_attention_backward(q, k, v, grad_out, full_idx, local_idx, *, window_
       ``dP = dO . v``, ``Delta = rowsum(P * dP)``, ``dS = P * (dP - Delta)``;
     * ``dq = scale * dS k``, ``dk = scale * dS^T q``, ``dv = P^T dO``, the last
       two summed over the query heads that share a KV head (V:124).
+
+    ``out`` (optional, the forward output handed to a backward) switches
+    Delta to the FlashAttention-2 convention ``Delta = rowsum(dO * out)``.
+    In exact arithmetic ``rowsum(P * dP) = dO . O`` (because ``O = P v``), so
+    the two agree for the exact O; with a rounded O they differ by
+    ``dO . (out - O)`` per row, and that difference moves dq_r by
+    ``-scale * (dO . (out - O)) * sum_j P_rj k_j`` (and dk alike).
+
+    ``delta_terms`` (optional dict) receives, per flattened query row and
+    query head, the exact ``Delta`` (``"delta"``, ``[T, Hq]``) and
+    ``sum_j P_rj k_j`` (``"pk"``, ``[T, Hq, D]``): the two factors of that
+    dq difference, for bounding it.
 
     A row with no legal key has P = 0 and contributes nothing.  Inputs are CPU
     tensors of the forward's shapes; returns ``(dq, dk, dv)`` in ``dtype``.
@@ -264,6 +298,10 @@ def routed_attention_backward(q, k, v, grad_out, full_idx, local_idx, *, window_
     kf = k.reshape(-1, hkv, d).to(dtype)
     vf = v.reshape(-1, hkv, d).to(dtype)
     dof = grad_out.reshape(batch * seq_q, hq, d).to(dtype)
+    of = None if out is None else out.reshape(batch * seq_q, hq, d).to(dtype)
+    if delta_terms is not None:
+        delta_terms["delta"] = torch.zeros(batch * seq_q, hq, dtype=dtype)
+        delta_terms["pk"] = torch.zeros(batch * seq_q, hq, d, dtype=dtype)
     dq = torch.zeros_like(qf)
     dk = torch.zeros_like(kf)
     dv = torch.zeros_like(vf)
@@ -294,7 +332,19 @@ def routed_attention_backward(q, k, v, grad_out, full_idx, local_idx, *, window_
         p = torch.where(tot > 0, e / torch.where(tot > 0, tot, torch.ones_like(tot)),
                         torch.zeros_like(e)).reshape(hkv, n * g, -1)       # [Hkv, R*G, L]
         dp = torch.bmm(dor, vc.transpose(1, 2).contiguous())                # [Hkv, R*G, L]
-        ds = _score_grad(p, dp)
+        delta = None
+        if of is not None:
+            # A row with no legal key has O = 0/0 = NaN and P = 0: it contributes
+            # nothing, so its Delta is taken as 0.
+            orr = of[rt].reshape(n, hkv, g, d).permute(1, 0, 2, 3).reshape(hkv, n * g, d)
+            delta = (dor * orr).sum(-1, keepdim=True)
+            delta = torch.where((tot > 0).reshape(hkv, n * g, 1), delta, torch.zeros_like(delta))
+        ds = _score_grad(p, dp, delta)
+        if delta_terms is not None:
+            ex = (p * dp).sum(-1)                                           # [Hkv, R*G]
+            delta_terms["delta"][rt] = ex.reshape(hkv, n, g).permute(1, 0, 2).reshape(n, hq)
+            pk = torch.bmm(p, kc)                                           # [Hkv, R*G, D]
+            delta_terms["pk"][rt] = pk.reshape(hkv, n, g, d).permute(1, 0, 2, 3).reshape(n, hq, d)
         dq_r = torch.bmm(ds, kc) * scale                                    # [Hkv, R*G, D]
         dq[rt] = dq_r.reshape(hkv, n, g, d).permute(1, 0, 2, 3).reshape(n, hq, d)
         dk[ks:ke] += (torch.bmm(ds.transpose(1, 2).contiguous(), qr) * scale).permute(1, 0, 2)

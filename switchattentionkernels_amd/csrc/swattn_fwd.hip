@@ -61,7 +61,8 @@
 //   longest causal item is long against the rest of the work (few KV heads,
 //   e.g. one GPU's share of a KV-head split, or short sequences on few
 //   heads), each full item runs as one workgroup per chunk of its range
-//   (4 to 64 key tiles, planned per call).  The chunks' fp32 O rows and
+//   (4 to 64 key tiles planned per call, longer for very long sequences so
+//   that the chunk slots stay near 2048).  The chunks' fp32 O rows and
 //   LSE go to the workspace and fwd_merge_kernel folds them (log2 LSE,
 //   V:236-241).  Chunk boundaries are fixed multiples of the chunk size,
 //   and an item inside one chunk is computed exactly as without a split.
@@ -123,7 +124,8 @@ struct FwdParams {
 };
 
 // Chunk of the key-range split, in 64-key tiles: between kSplitMinTiles and
-// kSplitTiles (4096 keys), chosen per call.  Boundaries sit at fixed
+// kSplitTiles (4096 keys), chosen per call, and longer for very long
+// sequences (split_plan keeps the chunk slots near kSplitMaxChunks).  Boundaries sit at fixed
 // multiples of it, so a row's chunks depend only on its own range, and an
 // item inside one chunk is computed exactly as without a split.
 constexpr int kSplitTiles = 64;

@@ -245,7 +245,7 @@ using namespace swattn;
 
 extern "C" {
 
-int swattn_version(void) { return (0 << 16) | 1; }
+int swattn_version(void) { return (0 << 16) | 2; }
 
 const char* swattn_last_error(void) { return g_last_error.c_str(); }
 

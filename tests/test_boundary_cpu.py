@@ -45,7 +45,7 @@ def test_library_exports_every_header_symbol():
 
 def test_version_and_workspace():
     lib = _lib.lib()
-    assert lib.swattn_version() >= 1
+    assert lib.swattn_version() == (0 << 16) | 2
     assert lib.swattn_compact_workspace_bytes(16384) == 0
     assert lib.swattn_compact_workspace_bytes(16385) == 2 * 4
     assert lib.swattn_compact_workspace_bytes(65536) == 4 * 4

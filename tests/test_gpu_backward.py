@@ -28,6 +28,7 @@ from switchattentionkernels_amd import (
     switch_gqa_prefill_backward,
     switch_gqa_prefill_forward,
     switch_gqa_prefill_varlen,
+    switch_gqa_prefill_varlen_forward,
     workloads,
 )
 from switchattentionkernels_amd.metadata import SwitchAttentionMetadata
@@ -346,3 +347,44 @@ def test_backward_with_no_query_rows():
     torch.cuda.synchronize()
     assert dq.shape == q.shape
     assert torch.count_nonzero(dk) == 0 and torch.count_nonzero(dv) == 0
+
+
+def test_backward_few_key_rows_delta_convention():
+    """Regression (found by a randomized sweep): two packed rows, cu_seqlens
+    [0, 2], Hq = Hkv = 1, window 2, every row local, seed 0 -- row 0 sees
+    one key, row 1 two.  The kernel takes Delta = dO . O from the bf16
+    forward output (the FlashAttention-2 convention), which moves dq of the
+    two-key row by 1.3-1.5e-2 relative L2 against the exact gradient: above
+    the plain 1e-2 bar, by a shift that is known exactly.
+
+    * Against the oracle with the same convention (Delta from the kernel's
+      own O), every gradient meets the plain bar.
+    * Against the exact gradient, each dq row lies within its Delta shift
+      scale * |dO . (O_bf16 - O)| * ||sum_j P_rj k_j|| (10 % slack) plus
+      1e-2 of its own norm plus a floor of 1e-2 of the rms row norm; the
+      CPU test ``test_delta_convention_shift_is_the_bound`` shows a dropped
+      or doubled Delta breaks that bound on this input."""
+    from test_oracle import _delta_bound_excess, _few_key_case
+    q, k, v, do, full_np, local_np, md_np = _few_key_case()
+    cu = [0, 2]
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    mask = torch.zeros(1, 2, dtype=torch.bool)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    o, lse = switch_gqa_prefill_varlen_forward(qd, kd, vd, full, local, cu, window_size=2)
+    md = build_switch_attention_metadata(2, 2, device=DEV, window_size=2, cu_seqlens=cu)
+    dq, dk, dv = switch_gqa_prefill_backward(qd, kd, vd, o, lse, do.to(DEV), full, local,
+                                             metadata=md, window_size=2)
+    torch.cuda.synchronize()
+    o_cpu = o.cpu()
+    conv = oracle.routed_attention_backward(q, k, v, do, full_np, local_np, metadata=md_np,
+                                            out=o_cpu)
+    for name, g, r in zip(("dq", "dk", "dv"), (dq, dk, dv), conv):
+        _grad_close(g, r, f"few-key {name} vs Delta-convention oracle")
+    terms = {}
+    exact = oracle.routed_attention_backward(q, k, v, do, full_np, local_np, metadata=md_np,
+                                             delta_terms=terms)
+    o_exact, _ = oracle.routed_attention(q, k, v, full_np, local_np, metadata=md_np)
+    rel = float((dq.float().cpu() - exact[0]).norm() / exact[0].norm())
+    excess = _delta_bound_excess(dq.float().cpu(), exact[0], o_cpu, o_exact, do, terms)
+    print(f"[grad] few-key dq vs exact: rel_l2 {rel:.3e}, bound excess {excess:.3e}", flush=True)
+    assert excess <= 0, f"dq row outside its Delta-convention bound by {excess:.3e}"

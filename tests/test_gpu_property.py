@@ -12,6 +12,11 @@ parity tests: O max-abs <= 2e-2, mean-abs <= 2e-3, LSE relative <= 1e-3,
 compaction bit-exact; gradients relative L2 <= 1e-2 and relative max <= 3e-2,
 each measured against max(|g_ref|, 1e-2) so that a gradient that is zero in
 exact arithmetic (a row that sees a single key) is held to an absolute bar.
+The gradient reference takes Delta = dO . O from the kernel's own bf16
+forward output, as the kernel does (the FlashAttention-2 convention): rows
+with one or two legal keys can otherwise sit just above 1e-2 by the known
+Delta shift (tests/test_gpu_backward.py bounds that shift against the exact
+gradient); the fixed-shape backward tests compare with the exact gradient.
 """
 
 import numpy as np
@@ -96,7 +101,8 @@ def test_backward_property(c):
                                         window_size=c["w"])
     torch.cuda.synchronize()
     f_np, l_np = R.compact(mask.numpy())
-    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, window_size=c["w"])
+    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, window_size=c["w"],
+                                            out=o.cpu())
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")
 
@@ -230,7 +236,8 @@ def test_varlen_property(c):
     f_np, l_np = R.compact(mask.numpy())
     o_ref, lse_ref = oracle.routed_attention(q, k, v, f_np, l_np, metadata=ref_md)
     _assert_close(o, lse, o_ref, lse_ref, tag=tag)
-    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, metadata=ref_md)
+    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, metadata=ref_md,
+                                            out=o.cpu())
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")
 
@@ -316,7 +323,7 @@ def test_backward_monotone_bounds_property(c):
     f_np, l_np = R.compact(mask.numpy())
     refs = oracle.routed_attention_backward(
         q, k, v, do, f_np, l_np,
-        metadata={"full_starts": fs, "local_starts": ls, "causal_ends": ce})
+        metadata={"full_starts": fs, "local_starts": ls, "causal_ends": ce}, out=o.cpu())
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")
 
@@ -374,6 +381,7 @@ def test_split_paths_property(c):
     o_ref, lse_ref = oracle.routed_attention(q, k, v, f_np, l_np, window_size=c["w"])
     _assert_close(o, lse, o_ref, lse_ref, tag=tag)
     _assert_close(o, lse, o_u.float().cpu(), lse_u.cpu(), tag=tag + " vs unsplit")
-    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, window_size=c["w"])
+    refs = oracle.routed_attention_backward(q, k, v, do, f_np, l_np, window_size=c["w"],
+                                            out=o.cpu())
     for name, g, r in zip(("dq", "dk", "dv"), grads, refs):
         _grad_close(g, r, f"{tag} {name}")

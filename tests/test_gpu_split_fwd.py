@@ -61,14 +61,17 @@ def _split_tiles(s, hq, hkv, w, n_full, n_local):
     """The chunk size (64-key tiles) of the library's split plan: 1.5 times
     the estimated key tiles per workgroup slot (full items at half a
     sequence, local ones at their window, over 512 slots), clamped to
-    [4, 64].  Used only to pick the rows that must come out bit-identical; a
-    wrong value here would fail the equality below."""
+    [4, 64], and at least what keeps the chunk slots (full items x KV heads x
+    sequence tiles / chunk) under 2048.  Used only to pick the rows that must
+    come out bit-identical; a wrong value here would fail the equality
+    below."""
     g = hq // hkv
     full_items, local_items = -(-n_full * g // 128), -(-n_local * g // 128)
     seq_tiles = -(-s // 64)
     local_tiles = -(-min(w, s) // 64) + 2
     est = hkv * (full_items * (seq_tiles // 2 + 2) + local_items * local_tiles)
-    return min(64, max(4, (3 * (est // 512)) // 2))
+    chunk = min(64, max(4, (3 * (est // 512)) // 2))
+    return max(chunk, -(-full_items * hkv * seq_tiles // 2048))
 
 
 def _case(seed, b, s, hq, hkv, p):
@@ -134,6 +137,7 @@ def test_items_spanning_many_sequences_run_whole():
     full, local = build_switch_query_indices(mask.to(DEV))
     o_s, l_s, base, big = _abi_forward(qd, kd, vd, full, local, w, split=True)
     print(f"sparse full list: workspace {base} -> {big}", flush=True)
+    assert big > base   # the split runs: the item is whole inside a split launch
     assert not torch.isnan(o_s).any() and not torch.isnan(l_s).any()
     f_np, l_np = R.compact(mask.numpy())
     rows = np.unique(np.concatenate([f_np, np.arange(0, b * s, 97)]))

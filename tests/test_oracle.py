@@ -554,9 +554,10 @@ def test_backward_planted_mistakes_are_caught(monkeypatch):
 
     assert pins()
     real = A._score_grad
-    monkeypatch.setattr(A, "_score_grad", lambda p, dp: p * dp)          # Delta dropped
+    monkeypatch.setattr(A, "_score_grad", lambda p, dp, delta=None: p * dp)   # Delta dropped
     assert not pins()
-    monkeypatch.setattr(A, "_score_grad", lambda p, dp: -real(p, dp))    # sign flipped
+    monkeypatch.setattr(A, "_score_grad",
+                        lambda p, dp, delta=None: -real(p, dp, delta))        # sign flipped
     assert not pins()
     monkeypatch.setattr(A, "_score_grad", real)
     # GQA head mapping flipped in every product
@@ -571,3 +572,58 @@ def test_backward_planted_mistakes_are_caught(monkeypatch):
     assert not pins()
     monkeypatch.setattr(A.torch, "bmm", real_bmm)
     assert pins()
+
+
+def _few_key_case():
+    """Two packed rows of one sequence (cu_seqlens [0, 2], Hq = Hkv = 1,
+    window 2, every row local), drawn as the GPU property sweep draws its
+    seed-0 case: row 0 sees one key, row 1 two."""
+    from switchattentionkernels_amd import workloads
+    gen = torch.Generator().manual_seed(0)
+    q, k, v = workloads.make_qkv(gen, 1, 2, 2, 1, 1, 128)
+    mask = torch.rand((1, 2), generator=gen) < 0.0
+    do = torch.randn(q.shape, generator=gen).to(torch.bfloat16)
+    full, local = R.compact(mask.numpy())
+    return q, k, v, do, full, local, R.varlen_metadata([0, 2], [0, 2], 2)
+
+
+def _delta_bound_excess(dq, dq_exact, out_used, out_exact, do, terms, rel=1e-2):
+    """max over rows of ||dq_r - dq_exact_r|| minus its allowance: the
+    Delta-convention shift (``delta_shift_bound``, with 10 % slack for the
+    rounding of the other terms) plus rel * ||dq_exact_r|| plus a floor of
+    rel times the rms row norm.  <= 0 passes."""
+    s = 128 ** -0.5
+    dev = (dq.double() - dq_exact.double()).reshape(-1, dq.shape[-2], 128).norm(dim=-1)
+    ref = dq_exact.double().reshape(-1, dq.shape[-2], 128).norm(dim=-1)
+    allow = (1.1 * A.delta_shift_bound(out_used, out_exact, do, terms["pk"], s)
+             + rel * ref + rel * float(ref.pow(2).mean().sqrt()))
+    return float((dev - allow).max())
+
+
+def test_delta_convention_shift_is_the_bound(monkeypatch):
+    """The FlashAttention-2 Delta (dO . out with out the bf16 forward output)
+    moves dq of a two-key row by 1.45e-2 relative L2 -- above a plain 1e-2 bar
+    -- and by exactly scale * |dO . (out - O)| * ||P k|| per row; a dropped or
+    doubled Delta lands far outside that bound."""
+    q, k, v, do, full, local, md = _few_key_case()
+    o, _ = A.routed_attention(q, k, v, full, local, metadata=md)
+    ob = o.to(torch.bfloat16)
+    terms = {}
+    ex = A.routed_attention_backward(q, k, v, do, full, local, metadata=md, delta_terms=terms)
+    conv = A.routed_attention_backward(q, k, v, do, full, local, metadata=md, out=ob)
+    rel = float((conv[0] - ex[0]).norm() / ex[0].norm())
+    assert rel > 1e-2                                  # the plain bar fails here
+    shift = A.delta_shift_bound(ob, o, do, terms["pk"], 128 ** -0.5)
+    dev = (conv[0] - ex[0]).double().reshape(-1, 1, 128).norm(dim=-1)
+    torch.testing.assert_close(dev, shift, rtol=1e-3, atol=1e-5)   # the shift is exact
+    assert _delta_bound_excess(conv[0], ex[0], ob, o, do, terms) <= 0
+    # The exact O as out gives the exact gradient.
+    same = A.routed_attention_backward(q, k, v, do, full, local, metadata=md, out=o)
+    torch.testing.assert_close(same[0], ex[0], atol=1e-6, rtol=1e-5)
+    real = A._score_grad
+    for planted in (lambda p, dp, delta=None: p * dp,                            # dropped
+                    lambda p, dp, delta=None: real(p, dp, 2 * delta)):           # doubled
+        monkeypatch.setattr(A, "_score_grad", planted)
+        bad = A.routed_attention_backward(q, k, v, do, full, local, metadata=md, out=ob)
+        assert _delta_bound_excess(bad[0], ex[0], ob, o, do, terms) > 0
+        monkeypatch.setattr(A, "_score_grad", real)
