@@ -67,10 +67,23 @@ def compile_flags() -> list[str]:
     ]
 
 
+GENERATED = [("gen_fwd_wide.py", "swattn_fwd_wide.inc")]
+
+
+def generate_sources() -> None:
+    """Run the assembly generators under ``csrc/`` (their outputs are
+    included by the HIP sources and are not kept in the repository)."""
+    for gen, out in GENERATED:
+        subprocess.run([sys.executable, os.path.join(CSRC, gen), os.path.join(CSRC, out)], check=True,
+                       stdout=subprocess.DEVNULL)
+
+
 def build(verbose: bool = False, out: str = LIB, extra_flags=(), sources=None) -> str:
     """Compile ``libswattn.so`` (or ``out``, with ``extra_flags`` appended to
     the compile flags; ``sources`` relative to ``csrc/``, default the
-    attention library's); returns its path.  Always recompiles."""
+    attention library's); returns its path.  Always regenerates the
+    generated includes and recompiles."""
+    generate_sources()
     cmd = [_hipcc()] + compile_flags() + list(extra_flags)
     tl = _torch_lib_dir()
     if tl is not None:

@@ -1,0 +1,1397 @@
+"""Generates the tile loop of ``fwd_wide_kernel`` as gfx950 assembly.
+
+Reference tags: V = swiattn_gqa_prefill_varlen.py.  The arithmetic is the
+reference branch kernel's hot loop (V:176-241): S = Q K^T, an online softmax
+in base 2 with c = sm_scale * log2(e) (V:207-221), P rounded to bf16 for P V
+while the row sum keeps the fp32 P (V:219-225), O = acc / l and
+LSE = log2(l) + m * c (V:236-241), written back to the listed rows only
+(V:243-249).
+
+Why generated assembly.  A work item here is 256 rows, 64 per wave, one
+wave per SIMD.  Per lane that needs the O accumulator (128 fp32), the Q^T
+operands (64 registers), two S tiles for the software pipeline (128), the
+packed P tile (32) and the K / V^T operand staging: more than the 256
+VGPRs a compiler-allocated kernel gets, and the compiler's MFMA register
+form is chosen per function, so it cannot keep O in AGPRs while S lives in
+VGPRs.  Written out here, O, Q^T and the LDS operands live in AGPRs (the
+matrix cores read and accumulate there directly) and S / P in VGPRs.
+
+Schedule.  One wave per SIMD issues everything in order, so the softmax
+must hide under the wave's own MFMAs.  Single-wave microbenchmarks on
+gfx950 show the rules the schedule follows: up to about five VALU
+instructions fit in the shadow of one 32x32x16 MFMA, a sixth costs a whole
+slot, and an exponential placed first behind an MFMA can stall the next
+one, so each MFMA slot takes at most one exponential and never as its
+first VALU instruction.  A 64-key tile has 64 exponentials and 64 MFMAs,
+so the exponentials must spread evenly over both GEMMs.  The online softmax
+therefore runs on 32-key halves of each tile (h = 0, 1; the running max
+moves at most per half): the scores of half 0 are final halfway through
+S = K Q^T, so its running max can be taken there and its exponentials can
+start as soon as P V of the previous tile does, which runs as two 16-MFMA
+halves.  Each step (tile j) is:
+
+  -- O, l *= 2^-e(j, 0) when some row's max moved in half 0 of tile j (rare) --
+  A  (32 MFMAs, S(j+1) half 0 then half 1):  the exponentials of P(j)
+     half 1, packing and row sums of P(j) half 0; then the running max of
+     S(j+1) half 0;
+  B1 (16 MFMAs, P(j) V(j) half 0):  the first 16 exponentials of S(j+1)
+     half 0, packing of P(j) half 1, the running max of S(j+1) half 1;
+  -- O, l *= 2^-e(j, 1) when some row's max moved in half 1 of tile j (rare) --
+  B2 (16 MFMAs, P(j) V(j) half 1):  the last 16 exponentials of S(j+1)
+     half 0, row sums of P(j) half 1; the ring slots move on, and the next
+     step's first K operands are read (before its barrier).
+
+Work a block cannot fit moves on to the next one (never past a rescale it
+must precede).  The running max is kept as n = -m c; a half's max x moves
+it only when d = x c + n exceeds 8 (P then stays below 2^8 without a
+move), and the rescale exponent e is d or 0.  Each lane keeps the partial
+row sum of its own 16 keys of each half; the two lanes of a row are added
+once, at the end.
+
+The output is one inline-asm string for ``swattn_fwd.hip``.  The generator
+places each block's VALU work into its MFMA slots with a list scheduler,
+inserts the ``s_waitcnt`` counts for its LDS and memory loads, and pads
+with ``s_nop`` wherever gfx950 needs independent instructions between
+dependent ones (the rules at the end, checked over the control-flow graph
+so that every path is covered).
+
+Register map (per lane; "rb" = row block 0/1 of the wave's 64 rows, "h" =
+32-key half of a 64-key tile, "db" = 32-wide block of head_dim):
+  a[0:127]    O^T accumulators, block (db, rb) at a[32 db + 16 rb]
+  a[128:191]  Q^T operands, k-step kk (16 of head_dim), rb at a[128 + 8 kk + 4 rb]
+  a[192:223]  K operands, eight sets (one per (h, kk) read)
+  a[224:247]  V^T operands, six sets
+  v[0:63], v[64:127]   S tiles (ping-pong), (rb, h) at +32 rb + 16 h
+  v[128:159]  P^T operands (bf16), k-step s2 (16 keys), rb at v[128 + 8 s2 + 4 rb]
+  v[160:167]  K operand LDS addresses per kk; v[168:171] V^T per s2
+  v[172:223]  row state and temporaries
+  v[224:255]  left to the compiler (the asm's inputs)
+"""
+
+from __future__ import annotations
+
+import re
+import sys
+
+# ---------------------------------------------------------------------------
+# registers
+# ---------------------------------------------------------------------------
+O_A, Q_A, KOP_A, VOP_A = 0, 128, 192, 224
+K_SETS, V_SETS = 8, 6      # LDS operand sets in flight
+S_V = (0, 64)
+PK_V = 128
+KOFF_V, VOFF_V = 160, 168
+V_L = 174                            # [rb] this lane's partial row sum
+V_AL = 176                           # rescale exponent [tile parity][h][rb] at 176 + 4 par + 2 h + rb
+V_NMC = 184                          # -m c after half h [h][rb] at 184 + 2 h + rb
+V_SPAN, V_KSR = 188, 190             # [rb]
+V_MXA, V_MXB = 192, 194              # [rb]
+V_NSENT = 199                        # -c times the max sentinel
+V_NINF = 200                         # -inf
+V_RS = 201                           # 201..208 rescale temporaries
+V_RA = 209                           # [rb] the exponent the rescale routine applies
+V_D, V_MT = 211, 213                 # [rb] running-max temporaries (V_D doubles as the mask's lo)
+V_MK = 217                           # 217..220 mask temporaries
+V_T = 188                            # epilogue temporaries (loop registers free by then)
+V_EPI = 209                          # 209..215 epilogue lane addresses
+V_LIMIT = 224                        # first VGPR left to the compiler
+
+# clobbered SGPRs
+S_RET = 52                  # return address of the rescale routine (2)
+S_FLAG = 54                 # rescale flags [tile parity][h] (2 each) at 54 + 4 par + 2 h
+S_T3, S_T4 = 62, 63
+S_WV, S_MK, S_MV = 64, 65, 66   # V^T DMA slot offset; M0 bases of this step's K / V^T DMAs
+S_T2 = 67
+S_WK, S_RK_OLD = 68, 69     # K DMA slot offset; the K read slot offset the address registers hold
+S_R, S_N = 70, 71           # step index r, tile count
+S_KPTR, S_KRL = 72, 74      # running K tile pointer (2), rows left (next K tile to stage)
+S_RK = 75                   # LDS offset of the K slot this step reads
+S_KRS, S_VRS = 76, 80       # K / V^T buffer descriptors (4 each)
+S_VPTR = 84                 # running V^T tile pointer (2)
+S_T0, S_T1 = 86, 87
+S_PAIRS = (88, 90, 92, 94)  # VALU compare results (2 each)
+S_MASK = 96                 # nonzero: this step's S(j+1) needs the range mask
+S_KEY0 = 98
+S_EIGHT, S_SENT = 99, 100   # 8.0 and the -2^30 max sentinel
+S_RV = 101                  # LDS offset (inside the V^T ring) of the V^T slot this step reads
+S_FIRST, S_LASTC = 52, 101  # clobbered range
+
+SENTINEL_BITS = 0xCE800000   # -2^30 as fp32 (V:174)
+NEG_INF_BITS = 0xFF800000
+EIGHT_BITS = 0x41000000
+RSRC_WORD3 = 0x00020000
+
+TILE_BYTES = 16384           # one K or V^T tile in LDS
+K_SLOTS = 4                  # K(j) staged three steps before it is read (so its first
+                             # operands can be read before the step's barrier)
+V_SLOTS = 3                  # V^T(j) staged two steps before it is read
+V_RING = K_SLOTS * TILE_BYTES  # byte offset of the V^T ring
+LDS_BYTES = V_RING + V_SLOTS * TILE_BYTES
+EPI_REGION = 32 * 272 + 128  # per-wave O staging for 32 rows + their offsets
+
+# ---------------------------------------------------------------------------
+# instructions
+# ---------------------------------------------------------------------------
+
+
+def vreg(i, n=1):
+    return f"v{i}" if n == 1 else f"v[{i}:{i + n - 1}]"
+
+
+def areg(i, n=1):
+    return f"a{i}" if n == 1 else f"a[{i}:{i + n - 1}]"
+
+
+def sreg(i, n=1):
+    return f"s{i}" if n == 1 else f"s[{i}:{i + n - 1}]"
+
+
+def regs(f, i, n):
+    return {f"{f}{i + k}" for k in range(n)}
+
+
+class Ins:
+    """One instruction with what the hazard and wait-count passes need."""
+
+    def __init__(self, text, kind, rd=(), wr=(), *, trans=False, lgkm=False, vm=False,
+                 mfma=None, mask_rd=(), branch=None, cond=False):
+        self.text = text
+        self.kind = kind          # mfma valu perm salu lds lds_w vmem_ld vmem_st dma nop wait barrier branch
+        self.rd = set(rd)
+        self.wr = set(wr)
+        self.trans = trans
+        self.lgkm = lgkm          # counted in lgkmcnt (LDS op)
+        self.vm = vm              # counted in vmcnt
+        self.mfma = mfma          # (dst_key, srcA regs, srcB regs, srcC regs or None)
+        self.mask_rd = set(mask_rd)
+        self.branch = branch      # target label
+        self.cond = cond          # conditional branch (falls through too)
+        self.urgent = False       # scheduled ahead of other ready work
+        self.feeds_trans = False  # computes the input of an exponential
+
+
+def mfma(dst, a, b, c_acc):
+    """dst / a / b = (file, first); c_acc: True accumulates into dst, False
+    starts from 0."""
+    df, di = dst
+    af, ai = a
+    bf, bi = b
+    dtxt = (vreg if df == "v" else areg)(di, 16)
+    atxt = (vreg if af == "v" else areg)(ai, 4)
+    btxt = (vreg if bf == "v" else areg)(bi, 4)
+    ctxt = dtxt if c_acc else "0"
+    dset = regs(df, di, 16)
+    ab = regs(af, ai, 4) | regs(bf, bi, 4)
+    rd = ab | (dset if c_acc else set())
+    return Ins(f"v_mfma_f32_32x32x16_bf16 {dtxt}, {atxt}, {btxt}, {ctxt}", "mfma", rd, dset,
+               mfma=((df, di), ab, dset if c_acc else None))
+
+
+def valu(text, rd, wr, trans=False, mask_rd=()):
+    return Ins(text, "valu", rd, wr, trans=trans, mask_rd=mask_rd)
+
+
+def salu(text, rd=(), wr=()):
+    return Ins(text, "salu", rd, wr)
+
+
+def label(name):
+    return Ins(f"{name}:", "label")
+
+
+def branch(op, target, cond=True):
+    return Ins(f"{op} {target}", "branch", branch=target, cond=cond)
+
+
+def waitcnt(vm=None, lgkm=None):
+    parts = []
+    if vm is not None:
+        parts.append(f"vmcnt({vm})")
+    if lgkm is not None:
+        parts.append(f"lgkmcnt({lgkm})")
+    return Ins("s_waitcnt " + " ".join(parts), "wait")
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+# ---------------------------------------------------------------------------
+
+
+def s_in(name):
+    return f"%[{name}]"
+
+
+def kop(h, kk):
+    return KOP_A + 4 * ((8 * h + kk) % K_SETS)
+
+
+def k_read(h, kk):
+    """K operand of k-step kk for the 32 keys of half h, from the K slot the
+    address registers point at."""
+    dst = kop(h, kk)
+    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(KOFF_V + kk)} offset:{h * 8192}",
+               "lds", {f"v{KOFF_V + kk}"}, regs("a", dst, 4), lgkm=True)
+
+
+def qk_mfmas(snxt, h, kk):
+    return [mfma(("v", snxt + 32 * rb + 16 * h), ("a", kop(h, kk)), ("a", Q_A + 8 * kk + 4 * rb), kk > 0)
+            for rb in range(2)]
+
+
+def vop(s2, db):
+    return VOP_A + 4 * ((4 * s2 + db) % V_SETS)
+
+
+def v_read(s2, db):
+    dst = vop(s2, db)
+    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(VOFF_V + s2)} offset:{db * 4096}",
+               "lds", {f"v{VOFF_V + s2}"}, regs("a", dst, 4), lgkm=True)
+
+
+def pv_mfmas(s2, db):
+    return [mfma(("a", O_A + 32 * db + 16 * rb), ("a", vop(s2, db)), ("v", PK_V + 8 * s2 + 4 * rb), True)
+            for rb in range(2)]
+
+
+V_SEQ = [(s2, db) for s2 in range(4) for db in range(4)]
+
+
+def dma(kind, i):
+    """One global -> LDS load of this wave's share of a K (kind 'k') or V^T
+    tile into the slot whose M0 base this step set up."""
+    rs = S_KRS if kind == "k" else S_VRS
+    mb = S_MK if kind == "k" else S_MV
+    off = s_in(f"{kind}dma{i}")
+    return [salu(f"s_add_u32 m0, {sreg(mb)}, {i * 1024}", wr={"m0"}),
+            Ins(f"buffer_load_dwordx4 {off}, {sreg(rs, 4)}, 0 offen lds", "dma",
+                regs("s", rs, 4) | {"m0"}, set(), vm=True)]
+
+
+def k_desc():
+    """K descriptor for tile r + 4 (empty past the last tile or the keys),
+    then advance the running pointer and row count by one tile."""
+    t0, t1 = sreg(S_T0), sreg(S_T1)
+    return [
+        salu(f"s_min_i32 {t0}, {sreg(S_KRL)}, {s_in('kmaxrows')}"),
+        salu(f"s_max_i32 {t0}, {t0}, 0"),
+        salu(f"s_mul_i32 {t0}, {t0}, {s_in('krowbytes')}"),
+        salu(f"s_add_u32 {t1}, {sreg(S_R)}, {K_SLOTS}"),
+        salu(f"s_cmp_lt_i32 {t1}, {sreg(S_N)}"),
+        salu(f"s_cselect_b32 {sreg(S_KRS + 2)}, {t0}, 0"),
+        salu(f"s_mov_b32 {sreg(S_KRS)}, {sreg(S_KPTR)}"),
+        salu(f"s_and_b32 {sreg(S_KRS + 1)}, {sreg(S_KPTR + 1)}, 0xffff"),
+        salu(f"s_mov_b32 {sreg(S_KRS + 3)}, {RSRC_WORD3:#x}"),
+        salu(f"s_add_u32 {sreg(S_KPTR)}, {sreg(S_KPTR)}, {s_in('ktilebytes')}"),
+        salu(f"s_addc_u32 {sreg(S_KPTR + 1)}, {sreg(S_KPTR + 1)}, 0"),
+        salu(f"s_sub_i32 {sreg(S_KRL)}, {sreg(S_KRL)}, 64"),
+    ]
+
+
+def v_desc():
+    """V^T descriptor for tile r + 2 (empty past the last tile), then advance."""
+    t1 = sreg(S_T1)
+    return [
+        salu(f"s_add_u32 {t1}, {sreg(S_R)}, 2"),
+        salu(f"s_cmp_lt_i32 {t1}, {sreg(S_N)}"),
+        salu(f"s_cselect_b32 {sreg(S_VRS + 2)}, {TILE_BYTES}, 0"),
+        salu(f"s_mov_b32 {sreg(S_VRS)}, {sreg(S_VPTR)}"),
+        salu(f"s_and_b32 {sreg(S_VRS + 1)}, {sreg(S_VPTR + 1)}, 0xffff"),
+        salu(f"s_mov_b32 {sreg(S_VRS + 3)}, {RSRC_WORD3:#x}"),
+        salu(f"s_add_u32 {sreg(S_VPTR)}, {sreg(S_VPTR)}, {TILE_BYTES}"),
+        salu(f"s_addc_u32 {sreg(S_VPTR + 1)}, {sreg(S_VPTR + 1)}, 0"),
+    ]
+
+
+def half_elems(s, h):
+    """The 32 registers of half h of the S tile at s, in packing order: for
+    each pair (i, i+1) of a row block's 16 registers, row block 0 then 1."""
+    out = []
+    for i in range(0, 16, 2):
+        for rb in range(2):
+            base = s + 32 * rb + 16 * h
+            out += [(rb, base + i), (rb, base + i + 1)]
+    return out
+
+
+def exps(s, h, lo, hi):
+    """P = 2^(s c - m c) in place for elements lo..hi-1 of half h."""
+    out = []
+    for rb, x in half_elems(s, h)[lo:hi]:
+        nmc = V_NMC + 2 * h + rb
+        out.append(valu(f"v_fma_f32 {vreg(x)}, {vreg(x)}, {s_in('c')}, {vreg(nmc)}",
+                        {f"v{x}", f"v{nmc}"}, {f"v{x}"}))
+        out[-1].feeds_trans = True
+        out.append(valu(f"v_exp_f32 {vreg(x)}, {vreg(x)}", {f"v{x}"}, {f"v{x}"}, trans=True))
+    return out
+
+
+def packs(s, h):
+    """P^T operands of half h packed to bf16: k-step s2 = 2 h + (i >= 8),
+    register (i % 8) / 2 holds keys i, i+1 of the row block."""
+    out = []
+    for i in range(0, 16, 2):
+        for rb in range(2):
+            base = s + 32 * rb + 16 * h
+            d = PK_V + 8 * (2 * h + (i >= 8)) + 4 * rb + (i % 8) // 2
+            out.append(valu(f"v_cvt_pk_bf16_f32 {vreg(d)}, {vreg(base + i)}, {vreg(base + i + 1)}",
+                            {f"v{base + i}", f"v{base + i + 1}"}, {f"v{d}"}))
+    return out
+
+
+def swap_combine(x, t, op):
+    """x = op(x, x of the lane 32 apart) (v_permlane32_swap)."""
+    return [valu(f"v_mov_b32 {vreg(t)}, {vreg(x)}", {f"v{x}"}, {f"v{t}"}),
+            Ins(f"v_permlane32_swap_b32 {vreg(x)}, {vreg(t)}", "perm", {f"v{x}", f"v{t}"},
+                {f"v{x}", f"v{t}"}),
+            valu(f"{op} {vreg(x)}, {vreg(x)}, {vreg(t)}", {f"v{x}", f"v{t}"}, {f"v{x}"})]
+
+
+def sums(s, h):
+    """Row sums of the fp32 P of half h (in place, after its packing), added
+    to this lane's partial l (the two lanes of a row keep partial sums of
+    their own keys; they are combined once, at the end)."""
+    out = []
+    width = 16
+    while width > 1:
+        hw = width // 2
+        for i in range(hw):
+            for rb in range(2):
+                b = s + 32 * rb + 16 * h
+                out.append(valu(f"v_add_f32 {vreg(b + i)}, {vreg(b + i)}, {vreg(b + i + hw)}",
+                                {f"v{b + i}", f"v{b + i + hw}"}, {f"v{b + i}"}))
+        width = hw
+    for rb in range(2):
+        b = s + 32 * rb + 16 * h
+        out.append(valu(f"v_add_f32 {vreg(V_L + rb)}, {vreg(V_L + rb)}, {vreg(b)}",
+                        {f"v{V_L + rb}", f"v{b}"}, {f"v{V_L + rb}"}))
+    return out
+
+
+def mask(s, h):
+    """Scores of half h outside each row's [start, end) set to -inf.
+    Register r of the half is key 32 h + 8 (r >> 2) + 4 hh + (r & 3) of the
+    tile; the row bounds were shifted by 4 hh, so it is legal iff
+    (off - lo) < span, unsigned, with lo = start - 4 hh - key0."""
+    out = []
+    for rb in range(2):
+        out.append(valu(f"v_subrev_u32 {vreg(V_D + rb)}, {sreg(S_KEY0)}, {vreg(V_KSR + rb)}",
+                        {f"v{V_KSR + rb}", f"s{S_KEY0}"}, {f"v{V_D + rb}"}))
+    elems = [(rb, r) for rb in range(2) for r in range(16)]
+    for g in range(0, len(elems), 4):
+        grp = elems[g:g + 4]
+        for k, (rb, r) in enumerate(grp):
+            off = 32 * h + 8 * (r >> 2) + (r & 3)
+            out.append(valu(f"v_sub_u32 {vreg(V_MK + k)}, {off}, {vreg(V_D + rb)}", {f"v{V_D + rb}"},
+                            {f"v{V_MK + k}"}))
+        for k, (rb, r) in enumerate(grp):
+            p = S_PAIRS[k]
+            out.append(valu(f"v_cmp_gt_u32_e64 {sreg(p, 2)}, {vreg(V_SPAN + rb)}, {vreg(V_MK + k)}",
+                            {f"v{V_SPAN + rb}", f"v{V_MK + k}"}, {f"s{p}", f"s{p + 1}"}))
+        for k, (rb, r) in enumerate(grp):
+            x = s + 32 * rb + 16 * h + r
+            p = S_PAIRS[k]
+            out.append(valu(f"v_cndmask_b32_e64 {vreg(x)}, {vreg(V_NINF)}, {vreg(x)}, {sreg(p, 2)}",
+                            {f"v{x}", f"v{V_NINF}"}, {f"v{x}"}, mask_rd={f"s{p}", f"s{p + 1}"}))
+    return out
+
+
+def running_max(s, h, par):
+    """Row max of half h of S, then the running max: with n = -m c of the
+    running max m (kept instead of m) and d = x c + n for the half's max x,
+    m moves to x only when d > 8 (the half's exponentials then stay below
+    2^8 without it); then n = -x c, and the half's rescale exponent is d
+    (O and l are multiplied by 2^-d), else 0.  The flag of (tile parity par,
+    h) is set when some row of the wave moved from a finite max (a row still
+    at the sentinel has O = 0 and l = 0).  Both row blocks' chains are
+    interleaved; all of it is marked urgent for the scheduler."""
+    chains = []
+    for rb in range(2):
+        b = s + 32 * rb + 16 * h
+        xa, xb = V_MXA + rb, V_MXB + rb
+        c = [valu(f"v_max3_f32 {vreg(xa)}, {vreg(b)}, {vreg(b + 1)}, {vreg(b + 2)}", regs("v", b, 3), {f"v{xa}"}),
+             valu(f"v_max3_f32 {vreg(xb)}, {vreg(b + 3)}, {vreg(b + 4)}, {vreg(b + 5)}", regs("v", b + 3, 3),
+                  {f"v{xb}"})]
+        acc = xa
+        for i in range(6, 16, 2):
+            c.append(valu(f"v_max3_f32 {vreg(acc)}, {vreg(acc)}, {vreg(b + i)}, {vreg(b + i + 1)}",
+                          {f"v{acc}", f"v{b + i}", f"v{b + i + 1}"}, {f"v{acc}"}))
+            acc = xb if acc == xa else xa
+        c.append(valu(f"v_max_f32 {vreg(xa)}, {vreg(xa)}, {vreg(xb)}", {f"v{xa}", f"v{xb}"}, {f"v{xa}"}))
+        c += swap_combine(xa, xb, "v_max_f32")
+        chains.append(c)
+    out = []
+    for a, b in zip(chains[0], chains[1]):
+        out += [a, b]
+    flag = S_FLAG + 4 * par + 2 * h
+    upd = []
+    for rb in range(2):
+        xa = V_MXA + rb
+        d, t = V_D + rb, V_MT + rb
+        pm, pq = S_PAIRS[2 * rb], S_PAIRS[2 * rb + 1]
+        nprev, nmc = V_NMC + 2 * (1 - h) + rb, V_NMC + 2 * h + rb
+        al = V_AL + 4 * par + 2 * h + rb
+        upd.append([
+            valu(f"v_fma_f32 {vreg(d)}, {vreg(xa)}, {s_in('c')}, {vreg(nprev)}", {f"v{xa}", f"v{nprev}"},
+                 {f"v{d}"}),
+            valu(f"v_cmp_neq_f32_e64 {sreg(pq, 2)}, {vreg(V_NSENT)}, {vreg(nprev)}",
+                 {f"v{V_NSENT}", f"v{nprev}"}, {f"s{pq}", f"s{pq + 1}"}),
+            valu(f"v_mul_f32 {vreg(t)}, {s_in('negc')}, {vreg(xa)}", {f"v{xa}"}, {f"v{t}"}),
+            valu(f"v_cmp_lt_f32_e64 {sreg(pm, 2)}, {sreg(S_EIGHT)}, {vreg(d)}", {f"v{d}", f"s{S_EIGHT}"},
+                 {f"s{pm}", f"s{pm + 1}"}),
+            valu(f"v_cndmask_b32_e64 {vreg(al)}, 0, {vreg(d)}, {sreg(pm, 2)}", {f"v{d}"}, {f"v{al}"},
+                 mask_rd={f"s{pm}", f"s{pm + 1}"}),
+            valu(f"v_cndmask_b32_e64 {vreg(nmc)}, {vreg(nprev)}, {vreg(t)}, {sreg(pm, 2)}",
+                 {f"v{nprev}", f"v{t}"}, {f"v{nmc}"}, mask_rd={f"s{pm}", f"s{pm + 1}"}),
+            salu(f"s_and_b64 {sreg(pq, 2)}, {sreg(pq, 2)}, {sreg(pm, 2)}", {f"s{pq}", f"s{pm}", f"s{pm + 1}"},
+                 {f"s{pq}", f"s{pq + 1}"}),
+        ])
+    for a, b in zip(upd[0], upd[1]):
+        out += [a, b]
+    out.append(salu(f"s_or_b64 {sreg(flag, 2)}, {sreg(S_PAIRS[1], 2)}, {sreg(S_PAIRS[3], 2)}",
+                    {f"s{S_PAIRS[1]}", f"s{S_PAIRS[3]}"}, {f"s{flag}", f"s{flag + 1}"}))
+    for x in out:
+        x.urgent = True
+    return out
+
+
+def rescale_routine():
+    """alpha = 2^-e for the rescale exponent e of each row (v[V_RA + rb],
+    0 for rows whose max did not move), then l *= alpha and O *= alpha;
+    entered by a branch with the return address in S_RET."""
+    out = []
+    for rb in range(2):
+        r = V_RA + rb
+        out.append(valu(f"v_exp_f32_e64 {vreg(r)}, -{vreg(r)}", {f"v{r}"}, {f"v{r}"}, trans=True))
+    for rb in range(2):
+        out.append(valu(f"v_mul_f32 {vreg(V_L + rb)}, {vreg(V_L + rb)}, {vreg(V_RA + rb)}",
+                        {f"v{V_L + rb}", f"v{V_RA + rb}"}, {f"v{V_L + rb}"}))
+    for rb in range(2):
+        for db in range(4):
+            for half in range(2):
+                base = O_A + 32 * db + 16 * rb + 8 * half
+                for k in range(8):
+                    out.append(valu(f"v_accvgpr_read_b32 {vreg(V_RS + k)}, {areg(base + k)}", {f"a{base + k}"},
+                                    {f"v{V_RS + k}"}))
+                for k in range(8):
+                    out.append(valu(f"v_mul_f32 {vreg(V_RS + k)}, {vreg(V_RS + k)}, {vreg(V_RA + rb)}",
+                                    {f"v{V_RS + k}", f"v{V_RA + rb}"}, {f"v{V_RS + k}"}))
+                for k in range(8):
+                    out.append(valu(f"v_accvgpr_write_b32 {areg(base + k)}, {vreg(V_RS + k)}", {f"v{V_RS + k}"},
+                                    {f"a{base + k}"}))
+    out.append(Ins(f"s_setpc_b64 {sreg(S_RET, 2)}", "ret"))
+    return out
+
+
+SLOT_CYCLES = 32
+VALU_ISSUE = 5
+LAT = {"valu": 8, "trans": 24, "perm": 12}
+SLOT_CAP = 5
+MF_LAT = 40          # cycles from an MFMA's issue to a VALU read of its result
+
+
+def _conflict(a, b):
+    """b must stay after a (program order) if they touch a common register
+    with at least one write."""
+    return bool(a.wr & (b.rd | b.wr | b.mask_rd) or b.wr & (a.rd | a.mask_rd))
+
+
+def schedule(mfmas, valu_list, side=None, lead_cap=4, carry=False, n_carried=0):
+    """Order one block: the MFMAs in their given order, side(i) (LDS reads,
+    DMAs) emitted before MFMA i and side(len) after the last, and the VALU /
+    SALU list (in a valid program order) placed into the MFMA slots by a
+    greedy list scheduler with a small cycle model.  Slot s is the gap after
+    MFMA s - 1 (slot 0: before the first).  VALU work that touches an MFMA's
+    registers stays after that MFMA (reading its result about one MFMA
+    later), and work that touches a side instruction's registers stays after
+    it; the first n_carried items come from the previous block instead and
+    go before any MFMA of this block whose registers they touch.  Each slot
+    takes at most SLOT_CAP VALU instructions and one exponential, never
+    first; exponentials, then urgent work, go first among what is ready.
+    With carry, what does not fit is returned for the next block instead of
+    being issued after the last MFMA."""
+    n = len(valu_list)
+    nm = len(mfmas)
+    sides = [side(i) if side is not None else [] for i in range(nm + 1)]
+    preds = [[] for _ in range(n)]
+    for j in range(n):
+        for i in range(j):
+            if _conflict(valu_list[i], valu_list[j]):
+                preds[j].append(i)
+    succs = [[] for _ in range(n)]
+    for j in range(n):
+        for i in preds[j]:
+            succs[i].append(j)
+    min_slot = [0] * n
+    deadline = [nm] * n
+    mf_users = [[] for _ in range(nm)]
+    for j, v in enumerate(valu_list):
+        for i, m in enumerate(mfmas):
+            if _conflict(m, v):
+                if j < n_carried:
+                    deadline[j] = min(deadline[j], i)
+                else:
+                    min_slot[j] = max(min_slot[j], i + 1)
+                    if m.wr & (v.rd | v.wr | v.mask_rd):
+                        mf_users[i].append(j)
+        for i in range(nm):
+            if any(_conflict(x, v) for x in sides[i]):
+                assert j >= n_carried or deadline[j] == nm
+                min_slot[j] = max(min_slot[j], i + 1 if i > 0 else 0)
+        if any(_conflict(x, v) for x in sides[nm]):
+            assert not carry, "a carried instruction conflicts with the block's last side work"
+    for j in range(n):
+        for k in preds[j]:
+            deadline[k] = min(deadline[k], deadline[j])
+    issued = [False] * n
+    npred = [len(p) for p in preds]
+    ready_at = [0] * n
+    out = []
+    state = {"t": 0, "done": 0, "fed": 0}
+
+    def pick(slot, slot_end, first, n_exp):
+        best = None
+        for j in range(n):
+            if issued[j] or npred[j] or min_slot[j] > slot:
+                continue
+            v = valu_list[j]
+            if v.trans and (first or n_exp >= 1):
+                continue
+            start = max(state["t"], ready_at[j])
+            if start + VALU_ISSUE > slot_end:
+                continue
+            lead = v.trans or (v.feeds_trans and state["fed"] < 2)
+            key = (start, not lead, not v.urgent, j)
+            if best is None or key < best[1]:
+                best = (j, key)
+        return None if best is None else (best[0], best[1][0])
+
+    def issue(j, start):
+        issued[j] = True
+        v = valu_list[j]
+        out.append(v)
+        state["t"] = start + (VALU_ISSUE if v.kind != "salu" else 1)
+        if v.feeds_trans:
+            state["fed"] += 1
+        if v.trans and state["fed"]:
+            state["fed"] -= 1
+        lat = LAT["trans"] if v.trans else LAT.get(v.kind, LAT["valu"])
+        for k in succs[j]:
+            npred[k] -= 1
+            ready_at[k] = max(ready_at[k], start + lat)
+        state["done"] += 1
+
+    def fill(slot, slot_end, cap):
+        first, n_exp, cnt = True, 0, 0
+        while cnt < cap:
+            b = pick(slot, slot_end, first, n_exp)
+            if b is None:
+                break
+            j, start = b
+            issue(j, start)
+            first = False
+            n_exp += valu_list[j].trans
+            cnt += valu_list[j].kind != "salu"
+
+    def force(i):
+        """Issue, in list order, the carried work MFMA i must follow."""
+        for j in range(n):
+            if not issued[j] and deadline[j] <= i:
+                assert npred[j] == 0
+                issue(j, max(state["t"], ready_at[j]))
+
+    out += sides[0]
+    fill(0, state["t"] + SLOT_CYCLES, lead_cap if mfmas else n)
+    for i, m in enumerate(mfmas):
+        if i > 0:
+            out += sides[i]
+        force(i)
+        out.append(m)
+        t0 = max(state["t"], i * SLOT_CYCLES)
+        for j in mf_users[i]:
+            ready_at[j] = max(ready_at[j], t0 + MF_LAT)
+        state["t"] = t0 + 2
+        remaining = n - state["done"]
+        slots_left = nm - i
+        cap = min(SLOT_CAP + 1, max(1, -(-remaining // slots_left)))
+        fill(i + 1, t0 + SLOT_CYCLES, cap)
+    left = []
+    if carry and nm:
+        left = [valu_list[j] for j in range(n) if not issued[j]]
+    else:
+        while state["done"] < n:
+            b = pick(nm + 1, 1 << 30, False, 0)
+            assert b is not None
+            issue(*b)
+    out += sides[nm]
+    return out, left
+
+
+# ---------------------------------------------------------------------------
+# blocks of a step
+# ---------------------------------------------------------------------------
+
+def block_a(par, kind, masked):
+    """S(j+1) = K(j+1) Q^T in 32 MFMAs (half 0, then half 1) while P(j)
+    half 1 is exponentiated, P(j) half 0 packed and summed, and S(j+1)
+    half 0's running max taken.  kind 'pre' (tile 0's S only), 'full',
+    'last' (no S(j+1)).  Returns (instructions, leftover VALU)."""
+    scur, snxt = S_V[par], S_V[1 - par]
+    pn = 1 - par           # parity of tile j + 1
+    out = []
+    dmas = []
+    if kind != "last":
+        out += k_desc()
+        dmas = [dma("k", i) for i in range(4)]
+    vl = []
+    if kind != "pre":
+        vl += exps(scur, 1, 0, 32) + packs(scur, 0) + sums(scur, 0)
+    if kind != "last":
+        if masked:
+            vl += mask(snxt, 0)
+        vl += running_max(snxt, 0, pn)
+    if kind == "last":
+        out += [v_read(*x) for x in V_SEQ[:V_SETS - 1]]
+        o, _ = schedule([], vl)
+        return out + o, []
+    mf = []
+    for h in range(2):
+        for kk in range(8):
+            mf += qk_mfmas(snxt, h, kk)
+    reads = [(h, kk) for h in range(2) for kk in range(8)]
+    pre = 4 if kind != "pre" else 0     # K operands read before the barrier
+
+    def side(i):
+        r = []
+        if i == 0:
+            r += [k_read(*x) for x in reads[pre:6]]
+        q = i // 2
+        if i % 2 == 1 and q + 6 < 16:
+            r.append(k_read(*reads[q + 6]))
+        if i % 8 == 4 and dmas:
+            r += dmas.pop(0)
+        if kind == "full" and 26 <= i <= 30:
+            r.append(v_read(*V_SEQ[i - 26]))
+        if i == len(mf):
+            for d in dmas:
+                r += d
+        return r
+    o, left = schedule(mf, vl, side, carry=True)
+    return out + o, left
+
+
+def block_b1(par, kind, masked, carried):
+    """P(j) V(j) for half 0 (16 MFMAs) while S(j+1) half 0 is exponentiated
+    (first 16 of 32), P(j) half 1 packed and S(j+1) half 1's running max
+    taken.  Returns (instructions, leftover VALU)."""
+    snxt = S_V[1 - par]
+    scur = S_V[par]
+    pn = 1 - par
+    out = []
+    dmas = []
+    if kind != "last":
+        out += v_desc()
+        dmas = [dma("v", i) for i in range(4)]
+    vl = list(carried)
+    nc = len(vl)
+    if kind != "last":
+        vl += exps(snxt, 0, 0, 16)
+    if kind != "pre":
+        vl += packs(scur, 1)
+    if kind != "last":
+        if masked:
+            vl += mask(snxt, 1)
+        vl += running_max(snxt, 1, pn)
+    if kind == "pre":
+        o, _ = schedule([], vl)
+        for d in dmas:
+            o += d
+        return out + o, []
+    mf = []
+    for s2 in (0, 1):
+        for db in range(4):
+            mf += pv_mfmas(s2, db)
+
+    def side(i):
+        r = []
+        q = i // 2
+        if i % 2 == 1 and q + V_SETS - 1 < 16:
+            r.append(v_read(*V_SEQ[q + V_SETS - 1]))
+        if i % 4 == 2 and dmas:
+            r += dmas.pop(0)
+        if i == len(mf):
+            for d in dmas:
+                r += d
+        return r
+    o, left = schedule(mf, vl, side, lead_cap=2, carry=True, n_carried=nc)
+    for x in left:
+        assert f"v{V_L}" not in x.wr, "the half-0 row sums must be added before the half-1 rescale"
+    return out + o, left
+
+
+def block_b2(par, kind, carried):
+    """P(j) V(j) for half 1 (16 MFMAs) while S(j+1) half 0's last 16
+    exponentials run and P(j) half 1 is summed; then the ring slots move on
+    and the next step's first K operands are read."""
+    scur, snxt = S_V[par], S_V[1 - par]
+    vl = list(carried)
+    nc = len(vl)
+    if kind != "last":
+        vl += exps(snxt, 0, 16, 32)
+    if kind != "pre":
+        vl += sums(scur, 1)
+    if kind != "last":
+        vl += rotate_slots()
+    mf = []
+    if kind != "pre":
+        for s2 in (2, 3):
+            for db in range(4):
+                mf += pv_mfmas(s2, db)
+
+    def side(i):
+        if i == len(mf):
+            return [k_read(0, kk) for kk in range(4)] if kind != "last" else []
+        q = 8 + i // 2
+        if i % 2 == 1 and q + V_SETS - 1 < 16:
+            return [v_read(*V_SEQ[q + V_SETS - 1])]
+        return []
+    o, _ = schedule(mf, vl, side, lead_cap=2, n_carried=nc)
+    return o
+
+
+# ---------------------------------------------------------------------------
+# program
+# ---------------------------------------------------------------------------
+
+
+class Block:
+    def __init__(self, name, ins, ret_point=False):
+        self.name = name
+        self.ins = ins
+        self.ret_point = ret_point    # the rescale routine may return here
+
+
+def rotate_slots():
+    """Step r -> r + 1: the K slot read and the K slot staged move one slot on
+    (four slots, offsets modulo 64 KiB); of the three V^T slots, the next
+    step reads the one V^T(r+1) went to (neither read nor staged in step r)
+    and stages into the one step r read.  The operand address registers move
+    with their slots; the M0 bases of the next step's DMAs follow."""
+    t0, t1 = sreg(S_T0), sreg(S_T1)
+    out = [
+        salu(f"s_add_u32 {sreg(S_RK)}, {sreg(S_RK)}, {TILE_BYTES}"),
+        salu(f"s_and_b32 {sreg(S_RK)}, {sreg(S_RK)}, {K_SLOTS * TILE_BYTES - 1}"),
+        salu(f"s_sub_u32 {t0}, {sreg(S_RK)}, {sreg(S_RK_OLD)}"),
+        salu(f"s_mov_b32 {sreg(S_RK_OLD)}, {sreg(S_RK)}"),
+        salu(f"s_add_u32 {sreg(S_WK)}, {sreg(S_WK)}, {TILE_BYTES}"),
+        salu(f"s_and_b32 {sreg(S_WK)}, {sreg(S_WK)}, {K_SLOTS * TILE_BYTES - 1}"),
+        salu(f"s_add_u32 {sreg(S_T2)}, {sreg(S_RV)}, {sreg(S_WV)}"),
+        salu(f"s_sub_u32 {sreg(S_T2)}, {V_SLOTS * TILE_BYTES}, {sreg(S_T2)}"),
+        salu(f"s_sub_u32 {t1}, {sreg(S_T2)}, {sreg(S_RV)}"),
+        salu(f"s_mov_b32 {sreg(S_WV)}, {sreg(S_RV)}"),
+        salu(f"s_mov_b32 {sreg(S_RV)}, {sreg(S_T2)}"),
+    ]
+    out += dma_bases()
+    for kk in range(8):
+        out.append(valu(f"v_add_u32 {vreg(KOFF_V + kk)}, {t0}, {vreg(KOFF_V + kk)}",
+                        {f"v{KOFF_V + kk}", f"s{S_T0}"}, {f"v{KOFF_V + kk}"}))
+    for s2 in range(4):
+        out.append(valu(f"v_add_u32 {vreg(VOFF_V + s2)}, {t1}, {vreg(VOFF_V + s2)}",
+                        {f"v{VOFF_V + s2}", f"s{S_T1}"}, {f"v{VOFF_V + s2}"}))
+    return out
+
+
+def dma_bases():
+    """M0 bases of a step's DMAs: K into S_WK, V^T into S_WV."""
+    return [salu(f"s_add_u32 {sreg(S_MK)}, {s_in('ldsw')}, {sreg(S_WK)}"),
+            salu(f"s_add_u32 {sreg(S_MV)}, {s_in('ldsw')}, {sreg(S_WV)}"),
+            salu(f"s_add_u32 {sreg(S_MV)}, {sreg(S_MV)}, {V_RING}")]
+
+
+def call_rescale(tag, par, h):
+    """Blocks that apply O, l *= 2^-e(tile of parity par, half h) when that
+    tile half's flag is set: test, then (rarely) copy the exponents, drain
+    the LDS reads and branch to the shared routine with the return
+    address."""
+    u = "%="
+    flag = S_FLAG + 4 * par + 2 * h
+    skip, pc = f"L{tag}_x_{u}", f"L{tag}_pc_{u}"
+    al = V_AL + 4 * par + 2 * h
+    test = Block(f"L{tag}_t_{u}", [salu(f"s_cmp_lg_u64 {sreg(flag, 2)}, 0"), branch("s_cbranch_scc0", skip)])
+    call = Block(f"L{tag}_c_{u}", [
+        valu(f"v_mov_b32 {vreg(V_RA)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA}"}),
+        valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al + 1)}", {f"v{al + 1}"}, {f"v{V_RA + 1}"}),
+        waitcnt(lgkm=0),
+        Ins(f"s_getpc_b64 {sreg(S_RET, 2)}", "salu", set(), {f"s{S_RET}", f"s{S_RET + 1}"}),
+        label(pc),
+        salu(f"s_add_u32 {sreg(S_RET)}, {sreg(S_RET)}, {skip}-{pc}"),
+        salu(f"s_addc_u32 {sreg(S_RET + 1)}, {sreg(S_RET + 1)}, 0"),
+        Ins(f"s_branch Lrescale_{u}", "call", branch=f"Lrescale_{u}", cond=False),
+    ])
+    return [test, call, Block(skip, [], ret_point=True)]
+
+
+def step_blocks(tag, par, kind, end_label):
+    """kind: 'pre' (S of the first tile only), 'full', 'last' (P V only).
+    A full step: wait and barrier, O, l *= alpha(j, 0) if needed, then an
+    unmasked or a masked copy of A, B1, O, l *= alpha(j, 1) if needed, B2."""
+    u = "%="
+    blocks = []
+    if kind == "pre":
+        # the first tile always takes the range mask (a no-op where all its
+        # keys are legal)
+        a, left = block_a(par, "pre", True)
+        b1, left = block_b1(par, "pre", True, left)
+        b2 = block_b2(par, "pre", left)
+        blocks.append(Block(f"L{tag}_a_{u}", mask_test() + a + b1 + b2))
+        return blocks
+    # DMAs issued two steps ago (and earlier) have landed in every wave; the
+    # 8 of the previous step may still be in flight, and so may the 4 K
+    # operand reads that step issued last (they read a slot no DMA of this
+    # step writes).
+    blocks.append(Block(f"L{tag}_s_{u}", [waitcnt(vm=8, lgkm=4), Ins("s_barrier", "barrier")]))
+    blocks += call_rescale(f"{tag}r0", par, 0)
+    if kind == "last":
+        a, left = block_a(par, "last", False)
+        b1, left = block_b1(par, "last", False, left)
+        blocks.append(Block(f"L{tag}_a_{u}", a + b1))
+        blocks += call_rescale(f"{tag}r1", par, 1)
+        blocks.append(Block(f"L{tag}_b2_{u}", block_b2(par, "last", left)))
+        blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
+        return blocks
+    blocks.append(Block(f"L{tag}_mt_{u}", mask_test() + [branch("s_cbranch_scc1", f"L{tag}_am_{u}")]))
+    for masked in (False, True):
+        mt = "m" if masked else "u"
+        a, left = block_a(par, kind, masked)
+        b1, left = block_b1(par, kind, masked, left)
+        blocks.append(Block(f"L{tag}_a{mt}_{u}", a + b1))
+        blocks += call_rescale(f"{tag}{mt}r1", par, 1)
+        blocks.append(Block(f"L{tag}_b2{mt}_{u}", block_b2(par, kind, left)))
+        if not masked:
+            blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
+    return blocks
+
+
+def prologue():
+    """Q rows into their AGPRs, O = 0, constants, LDS operand addresses, the
+    first three K tiles and the first V^T tile staged, then wait and barrier."""
+    # Every lane runs the loop; the compiler's code before this block wrote
+    # some of the input SGPRs with VALU instructions (v_readfirstlane), and a
+    # buffer instruction reading such an SGPR needs 5 wait states, which the
+    # compiler cannot see inside inline assembly.
+    out = [salu("s_mov_b64 exec, -1"), Ins("s_nop 7", "nop")]
+    for rb in range(2):
+        for kk in range(8):
+            d = Q_A + 8 * kk + 4 * rb
+            out.append(Ins(f"buffer_load_dwordx4 {areg(d, 4)}, {s_in(f'qoff{rb}')}, {s_in('qrsrc')}, 0 offen offset:{32 * kk}",
+                           "vmem_ld", set(), regs("a", d, 4), vm=True))
+    out += [
+        salu(f"s_mov_b32 {sreg(S_N)}, {s_in('ntiles')}"),
+        salu(f"s_mov_b64 {sreg(S_KPTR, 2)}, {s_in('kbase')}"),
+        salu(f"s_mov_b32 {sreg(S_KRL)}, {s_in('krows')}"),
+        salu(f"s_mov_b64 {sreg(S_VPTR, 2)}, {s_in('vbase')}"),
+        salu(f"s_mov_b32 {sreg(S_EIGHT)}, {EIGHT_BITS:#x}"),
+        salu(f"s_mov_b32 {sreg(S_SENT)}, {SENTINEL_BITS:#x}"),
+    ]
+    for f in range(4):
+        out.append(salu(f"s_mov_b64 {sreg(S_FLAG + 2 * f, 2)}, 0"))
+    # K(0..2) -> K slots 0..2 (descriptors for tile r + 4 with r = -4..-2),
+    # V^T(0) -> V^T slot 0 (tile r + 2 with r = -2).
+    for r, slot in ((-4, 0), (-3, 1), (-2, 2)):
+        out.append(salu(f"s_mov_b32 {sreg(S_R)}, {r}"))
+        out += k_desc()
+        out.append(salu(f"s_add_u32 {sreg(S_MK)}, {s_in('ldsw')}, {slot * TILE_BYTES}"))
+        for i in range(4):
+            out += dma("k", i)
+    out += v_desc()
+    out.append(salu(f"s_add_u32 {sreg(S_MV)}, {s_in('ldsw')}, {V_RING}"))
+    for i in range(4):
+        out += dma("v", i)
+    # State for step r = -1: K read slot 0, K staged into slot 3 (K(3)),
+    # V^T "read slot" 2 and V^T(1) staged into slot 1 (so that step 0 reads
+    # V^T slot 0 after the rotation).
+    out += [
+        salu(f"s_mov_b32 {sreg(S_R)}, -1"),
+        salu(f"s_mov_b32 {sreg(S_RK)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_RK_OLD)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_WK)}, {3 * TILE_BYTES}"),
+        salu(f"s_mov_b32 {sreg(S_RV)}, {2 * TILE_BYTES}"),
+        salu(f"s_mov_b32 {sreg(S_WV)}, {TILE_BYTES}"),
+    ]
+    out += dma_bases()
+    for i in range(128):
+        out.append(valu(f"v_accvgpr_write_b32 {areg(O_A + i)}, 0", set(), {f"a{O_A + i}"}))
+    for kk in range(8):
+        out.append(valu(f"v_xor_b32 {vreg(KOFF_V + kk)}, {32 * kk}, {s_in('kofs')}", set(), {f"v{KOFF_V + kk}"}))
+    for s2 in range(4):
+        out.append(valu(f"v_xor_b32 {vreg(VOFF_V + s2)}, {32 * s2}, {s_in('vofs')}", set(), {f"v{VOFF_V + s2}"}))
+        out.append(valu(f"v_add_u32 {vreg(VOFF_V + s2)}, {V_RING + 2 * TILE_BYTES}, {vreg(VOFF_V + s2)}",
+                        {f"v{VOFF_V + s2}"}, {f"v{VOFF_V + s2}"}))
+    for rb in range(2):
+        out += [
+            valu(f"v_mov_b32 {vreg(V_KSR + rb)}, {s_in(f'ksr{rb}')}", set(), {f"v{V_KSR + rb}"}),
+            valu(f"v_sub_u32 {vreg(V_SPAN + rb)}, {s_in(f'ker{rb}')}, {s_in(f'ksr{rb}')}", set(),
+                 {f"v{V_SPAN + rb}"}),
+            valu(f"v_max_i32 {vreg(V_SPAN + rb)}, 0, {vreg(V_SPAN + rb)}", {f"v{V_SPAN + rb}"},
+                 {f"v{V_SPAN + rb}"}),
+            valu(f"v_mov_b32 {vreg(V_L + rb)}, 0", set(), {f"v{V_L + rb}"}),
+        ]
+        for k in range(4):
+            out.append(valu(f"v_mov_b32 {vreg(V_AL + 2 * k + rb)}, 0", set(), {f"v{V_AL + 2 * k + rb}"}))
+    # n = -m c with m at the sentinel (no key seen yet)
+    out += [valu(f"v_mov_b32 {vreg(V_NSENT)}, {sreg(S_SENT)}", {f"s{S_SENT}"}, {f"v{V_NSENT}"}),
+            valu(f"v_mul_f32 {vreg(V_NSENT)}, {s_in('negc')}, {vreg(V_NSENT)}", {f"v{V_NSENT}"},
+                 {f"v{V_NSENT}"})]
+    for h in range(2):
+        for rb in range(2):
+            out.append(valu(f"v_mov_b32 {vreg(V_NMC + 2 * h + rb)}, {vreg(V_NSENT)}", {f"v{V_NSENT}"},
+                            {f"v{V_NMC + 2 * h + rb}"}))
+    out.append(valu(f"v_mov_b32 {vreg(V_NINF)}, {NEG_INF_BITS:#x}", set(), {f"v{V_NINF}"}))
+    out += [waitcnt(vm=0), Ins("s_barrier", "barrier")]
+    return out
+
+
+def epilogue():
+    """LSE = log2(l) + m c per row; O = acc / l as bf16 rows, staged through
+    this wave's LDS region (32 rows at a 272-byte stride, then their 32 byte
+    offsets) so that each store writes whole 256-byte rows."""
+    out = [waitcnt(vm=0, lgkm=0), Ins("s_barrier", "barrier")]
+    E = V_EPI
+    lane = s_in("lane")
+    # E+0: write base (row rl, hh half) ; E+1: offset-table slot of row rl
+    # E+2: read base (row lane>>4, chunk lane&15) ; E+3: offset-table read base
+    # E+4: 16 * (lane & 15) ; E+5, E+6: temporaries
+    t5, t6 = E + 5, E + 6
+    out += [
+        valu(f"v_and_b32 {vreg(t5)}, 31, {lane}", set(), {f"v{t5}"}),
+        valu(f"v_lshrrev_b32 {vreg(t6)}, 5, {lane}", set(), {f"v{t6}"}),
+        valu(f"v_mul_u32_u24 {vreg(E)}, 0x110, {vreg(t5)}", {f"v{t5}"}, {f"v{E}"}),
+        valu(f"v_lshl_add_u32 {vreg(E)}, {vreg(t6)}, 3, {vreg(E)}", {f"v{t6}", f"v{E}"}, {f"v{E}"}),
+        valu(f"v_add_u32 {vreg(E)}, {s_in('ebase')}, {vreg(E)}", {f"v{E}"}, {f"v{E}"}),
+        valu(f"v_lshl_add_u32 {vreg(E + 1)}, {vreg(t5)}, 2, {s_in('ebase')}", {f"v{t5}"}, {f"v{E + 1}"}),
+        valu(f"v_add_u32 {vreg(E + 1)}, {32 * 272}, {vreg(E + 1)}", {f"v{E + 1}"}, {f"v{E + 1}"}),
+        valu(f"v_lshrrev_b32 {vreg(t6)}, 4, {lane}", set(), {f"v{t6}"}),
+        valu(f"v_and_b32 {vreg(E + 4)}, 15, {lane}", set(), {f"v{E + 4}"}),
+        valu(f"v_lshlrev_b32 {vreg(E + 4)}, 4, {vreg(E + 4)}", {f"v{E + 4}"}, {f"v{E + 4}"}),
+        valu(f"v_mul_u32_u24 {vreg(E + 2)}, 0x110, {vreg(t6)}", {f"v{t6}"}, {f"v{E + 2}"}),
+        valu(f"v_add3_u32 {vreg(E + 2)}, {s_in('ebase')}, {vreg(E + 2)}, {vreg(E + 4)}",
+             {f"v{E + 2}", f"v{E + 4}"}, {f"v{E + 2}"}),
+        valu(f"v_lshl_add_u32 {vreg(E + 3)}, {vreg(t6)}, 2, {s_in('ebase')}", {f"v{t6}"}, {f"v{E + 3}"}),
+        valu(f"v_add_u32 {vreg(E + 3)}, {32 * 272}, {vreg(E + 3)}", {f"v{E + 3}"}, {f"v{E + 3}"}),
+    ]
+    il = (V_T + 8, V_T + 9)
+    for rb in range(2):
+        out += swap_combine(V_L + rb, V_T + 2 + rb, "v_add_f32")
+    for rb in range(2):
+        t = V_T + rb
+        nmc = V_NMC + 2 + rb      # -m c after the last half
+        out += [
+            valu(f"v_log_f32 {vreg(t)}, {vreg(V_L + rb)}", {f"v{V_L + rb}"}, {f"v{t}"}, trans=True),
+            valu(f"v_sub_f32 {vreg(t)}, {vreg(t)}, {vreg(nmc)}", {f"v{nmc}", f"v{t}"}, {f"v{t}"}),
+            Ins(f"buffer_store_dword {vreg(t)}, {s_in(f'lsoff{rb}')}, {s_in('lrsrc')}, 0 offen", "vmem_st",
+                {f"v{t}"}, set(), vm=True),
+            valu(f"v_rcp_f32 {vreg(il[rb])}, {vreg(V_L + rb)}", {f"v{V_L + rb}"}, {f"v{il[rb]}"}, trans=True),
+        ]
+    for rb in range(2):
+        if rb == 1:
+            out.append(waitcnt(lgkm=0))
+        for db in range(4):
+            for j in range(4):
+                a0 = O_A + 32 * db + 16 * rb + 4 * j
+                tv = 8 * (4 * db + j) % 64   # rotate through v[0:63]
+                for k in range(4):
+                    out.append(valu(f"v_accvgpr_read_b32 {vreg(tv + k)}, {areg(a0 + k)}", {f"a{a0 + k}"},
+                                    {f"v{tv + k}"}))
+                for k in range(4):
+                    out.append(valu(f"v_mul_f32 {vreg(tv + k)}, {vreg(tv + k)}, {vreg(il[rb])}",
+                                    {f"v{tv + k}", f"v{il[rb]}"}, {f"v{tv + k}"}))
+                out.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 4)}, {vreg(tv)}, {vreg(tv + 1)}",
+                                {f"v{tv}", f"v{tv + 1}"}, {f"v{tv + 4}"}))
+                out.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 5)}, {vreg(tv + 2)}, {vreg(tv + 3)}",
+                                {f"v{tv + 2}", f"v{tv + 3}"}, {f"v{tv + 5}"}))
+                out.append(Ins(f"ds_write_b64 {vreg(E)}, {vreg(tv + 4, 2)} offset:{64 * db + 16 * j}", "lds_w",
+                               {f"v{E}", f"v{tv + 4}", f"v{tv + 5}"}, set(), lgkm=True))
+        out.append(Ins(f"ds_write_b32 {vreg(E + 1)}, {s_in(f'ooff{rb}')}", "lds_w", {f"v{E + 1}"}, set(),
+                       lgkm=True))
+        out.append(waitcnt(lgkm=0))
+        for i in range(8):
+            out.append(Ins(f"ds_read_b32 {vreg(64 + i)}, {vreg(E + 3)} offset:{16 * i}", "lds",
+                           {f"v{E + 3}"}, {f"v{64 + i}"}, lgkm=True))
+            out.append(Ins(f"ds_read_b128 {vreg(72 + 4 * i, 4)}, {vreg(E + 2)} offset:{4 * 272 * i}", "lds",
+                           {f"v{E + 2}"}, regs("v", 72 + 4 * i, 4), lgkm=True))
+        for i in range(8):
+            out.append(valu(f"v_add_u32 {vreg(64 + i)}, {vreg(64 + i)}, {vreg(E + 4)}",
+                            {f"v{64 + i}", f"v{E + 4}"}, {f"v{64 + i}"}))
+            out.append(Ins(f"buffer_store_dwordx4 {vreg(72 + 4 * i, 4)}, {vreg(64 + i)}, {s_in('orsrc')}, 0 offen",
+                           "vmem_st", regs("v", 72 + 4 * i, 4) | {f"v{64 + i}"}, set(), vm=True))
+    return out
+
+
+def mask_test():
+    """S_KEY0 = first key of tile r + 1; SCC = that tile needs the range
+    mask (it lies outside [it0, it1))."""
+    t1 = sreg(S_T1)
+    return [salu(f"s_add_u32 {t1}, {sreg(S_R)}, 1"),
+            salu(f"s_lshl_b32 {sreg(S_KEY0)}, {t1}, 6"),
+            salu(f"s_add_u32 {sreg(S_KEY0)}, {sreg(S_KEY0)}, {s_in('key0')}"),
+            salu(f"s_cmp_lt_i32 {t1}, {s_in('it0')}"),
+            salu(f"s_cselect_b32 {sreg(S_MASK)}, 1, 0"),
+            salu(f"s_cmp_ge_i32 {t1}, {s_in('it1')}"),
+            salu(f"s_cselect_b32 {sreg(S_T0)}, 1, 0"),
+            salu(f"s_or_b32 {sreg(S_MASK)}, {sreg(S_MASK)}, {sreg(S_T0)}"),
+            salu(f"s_cmp_lg_u32 {sreg(S_MASK)}, 0")]
+
+
+def program():
+    u = "%="
+    blocks = [Block(f"Lpro_{u}", prologue() + [salu(f"s_cmp_le_i32 {sreg(S_N)}, 0"),
+                                                  branch("s_cbranch_scc1", f"Lepi_{u}")])]
+    blocks += step_blocks("p", 1, "pre", None)
+    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R)}, 0")]))
+    t1 = sreg(S_T1)
+    for par in (0, 1):
+        blocks.append(Block(f"Lt{par}_{u}", [salu(f"s_add_u32 {t1}, {sreg(S_R)}, 1"),
+                                            salu(f"s_cmp_ge_i32 {t1}, {sreg(S_N)}"),
+                                            branch("s_cbranch_scc1", f"Llast{par}_{u}")]))
+        blocks += step_blocks(f"f{par}", par, "full", f"Linc{par}_{u}")
+        tail = [salu(f"s_add_u32 {sreg(S_R)}, {sreg(S_R)}, 1")]
+        if par == 1:
+            tail.append(branch("s_branch", f"Lt0_{u}", cond=False))
+        blocks.append(Block(f"Linc{par}_{u}", tail))
+    for par in (0, 1):
+        bl = step_blocks(f"l{par}", par, "last", f"Lepi_{u}")
+        bl[0].name = f"Llast{par}_{u}"
+        blocks += bl
+    # the shared rescale routine (reached only by branches)
+    blocks.append(Block(f"Lrescale_{u}", rescale_routine()))
+    blocks.append(Block(f"Lepi_{u}", epilogue()))
+    return blocks
+
+
+# ---------------------------------------------------------------------------
+# hazard padding over the control-flow graph, and wait counts
+# ---------------------------------------------------------------------------
+
+SAT = 64
+MFMA_RAW = 12       # XDL 8-pass result -> any non-MFMA read, or a non-MFMA overwrite
+VALU_TO_MFMA = 2    # VALU write -> MFMA operand read
+VALU_SGPR_MASK = 2  # VALU write of an SGPR pair -> VALU read of it as lane mask / carry
+VALU_TO_PERM = 2    # VALU write -> v_permlane32_swap read
+TRANS_FWD = 1       # transcendental result -> next VALU read
+M0_TO_DMA = 1       # SALU write of M0 -> LDS DMA
+AB_WAR = 4          # margin: MFMA srcA/B read -> overwrite
+
+
+class HState:
+    def __init__(self):
+        self.mf_w = {}      # reg -> (dist, dst key)
+        self.mf_ab = {}     # reg -> dist since an MFMA read it as srcA/B
+        self.valu_w = {}    # reg -> dist since a VALU wrote it
+        self.trans_w = {}
+        self.m0 = SAT
+
+    def copy(self):
+        h = HState()
+        h.mf_w = dict(self.mf_w)
+        h.mf_ab = dict(self.mf_ab)
+        h.valu_w = dict(self.valu_w)
+        h.trans_w = dict(self.trans_w)
+        h.m0 = self.m0
+        return h
+
+    def advance(self, n):
+        for d in (self.valu_w, self.trans_w, self.mf_ab):
+            for k in list(d):
+                v = d[k] + n
+                if v >= SAT:
+                    del d[k]
+                else:
+                    d[k] = v
+        for k in list(self.mf_w):
+            v, key = self.mf_w[k]
+            v += n
+            if v >= SAT:
+                del self.mf_w[k]
+            else:
+                self.mf_w[k] = (v, key)
+        self.m0 = min(SAT, self.m0 + n)
+
+    def merge(self, o):
+        h = self.copy()
+        for k, v in o.valu_w.items():
+            h.valu_w[k] = min(v, h.valu_w.get(k, SAT))
+        for k, v in o.trans_w.items():
+            h.trans_w[k] = min(v, h.trans_w.get(k, SAT))
+        for k, v in o.mf_ab.items():
+            h.mf_ab[k] = min(v, h.mf_ab.get(k, SAT))
+        for k, (v, key) in o.mf_w.items():
+            if k in h.mf_w:
+                v0, key0 = h.mf_w[k]
+                h.mf_w[k] = (min(v, v0), key if key == key0 else None)
+            else:
+                h.mf_w[k] = (v, key)
+        h.m0 = min(h.m0, o.m0)
+        return h
+
+    def key(self):
+        return (tuple(sorted(self.mf_w.items())), tuple(sorted(self.mf_ab.items())),
+                tuple(sorted(self.valu_w.items())), tuple(sorted(self.trans_w.items())), self.m0)
+
+
+def need(ins, h):
+    """Wait states that must separate ins from what came before."""
+    n = 0
+    if ins.kind == "mfma":
+        dkey, ab, csrc = ins.mfma
+        for r in ab:
+            if r in h.mf_w:
+                n = max(n, MFMA_RAW - h.mf_w[r][0])
+            if r in h.valu_w:
+                n = max(n, VALU_TO_MFMA - h.valu_w[r])
+        if csrc:
+            for r in csrc:
+                if r in h.mf_w:
+                    d, key = h.mf_w[r]
+                    if key != dkey:
+                        n = max(n, MFMA_RAW - d)
+                if r in h.valu_w:
+                    n = max(n, VALU_TO_MFMA - h.valu_w[r])
+        for r in ins.wr:
+            if r in h.valu_w:
+                n = max(n, VALU_TO_MFMA - h.valu_w[r])
+            if not csrc and r in h.mf_w:
+                n = max(n, MFMA_RAW - h.mf_w[r][0])
+        return n
+    for r in ins.rd | ins.mask_rd:
+        if r in h.mf_w:
+            n = max(n, MFMA_RAW - h.mf_w[r][0])
+    for r in ins.wr:
+        if r in h.mf_w:
+            n = max(n, MFMA_RAW - h.mf_w[r][0])
+        if r in h.mf_ab:
+            n = max(n, AB_WAR - h.mf_ab[r])
+    if ins.kind in ("valu", "perm"):
+        for r in ins.mask_rd | {x for x in ins.rd if x.startswith("s")}:
+            if r in h.valu_w:
+                n = max(n, VALU_SGPR_MASK - h.valu_w[r])
+        if ins.kind == "perm":
+            for r in ins.rd:
+                if r in h.valu_w:
+                    n = max(n, VALU_TO_PERM - h.valu_w[r])
+        if not ins.trans:
+            for r in ins.rd:
+                if r in h.trans_w:
+                    n = max(n, TRANS_FWD - h.trans_w[r])
+    if ins.kind == "dma":
+        n = max(n, M0_TO_DMA - h.m0)
+    return max(n, 0)
+
+
+def apply(ins, h):
+    if ins.kind == "label":
+        return
+    if ins.kind == "nop":
+        h.advance(int(ins.text.split()[1]) + 1)
+        return
+    h.advance(1)
+    if ins.kind == "mfma":
+        dkey, ab, csrc = ins.mfma
+        for r in ins.wr:
+            h.mf_w[r] = (0, dkey)
+            h.valu_w.pop(r, None)
+        for r in ab:
+            h.mf_ab[r] = 0
+        return
+    for r in ins.wr:
+        if r == "m0":
+            h.m0 = 0
+        h.mf_w.pop(r, None)
+        if ins.kind in ("valu", "perm"):
+            h.valu_w[r] = 0
+            if ins.trans:
+                h.trans_w[r] = 0
+            else:
+                h.trans_w.pop(r, None)
+        else:
+            h.valu_w.pop(r, None)
+            h.trans_w.pop(r, None)
+
+
+def pad_block(ins_list, h):
+    out = []
+    for ins in ins_list:
+        n = need(ins, h)
+        while n > 0:
+            k = min(n, 16)
+            nop = Ins(f"s_nop {k - 1}", "nop")
+            out.append(nop)
+            apply(nop, h)
+            n -= k
+        out.append(ins)
+        apply(ins, h)
+    return out
+
+
+def successors(blocks):
+    names = {b.name: i for i, b in enumerate(blocks)}
+    succ = []
+    for i, b in enumerate(blocks):
+        s = []
+        last = b.ins[-1] if b.ins else None
+        if last is not None and last.kind in ("branch", "call"):
+            s.append(names[last.branch])
+            if last.cond and i + 1 < len(blocks):
+                s.append(i + 1)
+        elif last is not None and last.kind == "ret":
+            s += [k for k, x in enumerate(blocks) if x.ret_point]
+        elif i + 1 < len(blocks):
+            s.append(i + 1)
+        succ.append(s)
+    return succ
+
+
+def pad_program(blocks):
+    succ = successors(blocks)
+    preds = [[] for _ in blocks]
+    for i, s in enumerate(succ):
+        for j in s:
+            preds[j].append(i)
+    entry = [None] * len(blocks)
+    entry[0] = HState()
+    exit_ = [None] * len(blocks)
+    padded = [None] * len(blocks)
+    work = list(range(len(blocks)))
+    while work:
+        i = work.pop(0)
+        h = None
+        for p in preds[i]:
+            if exit_[p] is not None:
+                h = exit_[p] if h is None else h.merge(exit_[p])
+        if i == 0:
+            h = HState()
+        if h is None:
+            continue
+        if entry[i] is not None and entry[i].key() == h.key() and padded[i] is not None:
+            continue
+        entry[i] = h
+        hh = h.copy()
+        padded[i] = pad_block(blocks[i].ins, hh)
+        exit_[i] = hh
+        for j in succ[i]:
+            if j not in work:
+                work.append(j)
+    for i, b in enumerate(blocks):
+        assert padded[i] is not None, f"unreachable block {b.name}"
+    return padded
+
+
+def insert_waits(blocks):
+    """s_waitcnt lgkmcnt(n) before each use of an LDS read's result, with n
+    the number of LDS operations issued after that read.  The queue of
+    outstanding LDS operations is carried along the control-flow graph; every
+    block's predecessors must agree on it (checked).  Results of memory loads
+    (the Q rows) are only used after a vmcnt(0); the DMAs write no
+    registers and are waited for explicitly at each step."""
+    succ = successors(blocks)
+    entry = [None] * len(blocks)
+    entry[0] = ([], set())
+    out = []
+    for i, b in enumerate(blocks):
+        assert entry[i] is not None, f"block {b.name} has no forward predecessor"
+        lg = [set(x) for x in entry[i][0]]
+        pend_vm = set(entry[i][1])          # registers of loads not yet waited for
+        res = []
+        for ins in b.ins:
+            if ins.kind == "wait":
+                mm = re.search(r"lgkmcnt\((\d+)\)", ins.text)
+                if mm:
+                    k = int(mm.group(1))
+                    lg = lg[len(lg) - k:] if 0 < k < len(lg) else ([] if k == 0 else lg)
+                if "vmcnt(0)" in ins.text:
+                    pend_vm = set()
+                res.append(ins)
+                continue
+            uses = ins.rd | ins.mask_rd | ins.wr
+            assert not (uses & pend_vm), f"memory load result used before vmcnt(0): {ins.text}"
+            w_l = None
+            for k, regset in enumerate(lg):
+                if regset & uses:
+                    w_l = len(lg) - k - 1
+            if w_l is not None:
+                res.append(waitcnt(lgkm=w_l))
+                lg = lg[len(lg) - w_l:] if w_l > 0 else []
+            if ins.lgkm and len(lg) >= 15:      # the lgkmcnt field holds at most 15
+                res.append(waitcnt(lgkm=7))
+                lg = lg[len(lg) - 7:]
+            res.append(ins)
+            if ins.lgkm:
+                lg.append(set(ins.wr))
+            if ins.kind == "vmem_ld":
+                pend_vm |= ins.wr
+        out.append(res)
+        state = ([set(x) for x in lg], set(pend_vm))
+        for j in succ[i]:
+            if entry[j] is None:
+                entry[j] = state
+                continue
+            m = _merge_queues(entry[j], state)
+            assert m is not None, f"LDS queues differ into {blocks[j].name}"
+            assert j > i or m == entry[j], f"back edge with a longer LDS queue into {blocks[j].name}"
+            entry[j] = m
+    return out
+
+
+def _merge_queues(a, b):
+    """Entry state of a block reached with LDS queues a and b: the longer
+    one, when the shorter is its tail (a wait counted against the longer
+    queue is then also enough for the shorter); None otherwise."""
+    if a[1] != b[1]:
+        return None
+    la, lb = a[0], b[0]
+    if len(la) < len(lb):
+        la, lb = lb, la
+        a, b = b, a
+    if lb and la[len(la) - len(lb):] != lb:
+        return None
+    return a
+
+
+def generate():
+    blocks = program()
+    waited = insert_waits(blocks)
+    for b, w in zip(blocks, waited):
+        b.ins = w
+    padded = pad_program(blocks)
+    lines = []
+    for b, ins_list in zip(blocks, padded):
+        lines.append(f"{b.name}:")
+        for ins in ins_list:
+            lines.append("  " + ins.text)
+    return lines
+
+
+def clobbers():
+    c = [f"v{i}" for i in range(V_LIMIT)] + [f"a{i}" for i in range(256)]
+    c += [f"s{i}" for i in range(S_FIRST, S_LASTC + 1)]
+    c += ["vcc", "exec", "m0", "memory"]
+    return c
+
+
+def emit(path):
+    lines = generate()
+    with open(path, "w") as f:
+        f.write("// Generated by gen_fwd_wide.py: the tile loop of fwd_wide_kernel.  Do not edit.\n")
+        f.write("#pragma once\n")
+        f.write("#define SWATTN_FWD_WIDE_ASM \\\n")
+        for ln in lines:
+            f.write(f'  "{ln}\\n" \\\n')
+        f.write('  ""\n')
+        f.write(f"#define SWATTN_FWD_WIDE_LDS_BYTES {LDS_BYTES}\n")
+        f.write("#define SWATTN_FWD_WIDE_CLOBBERS \\\n  ")
+        f.write(", ".join(f'"{x}"' for x in clobbers()))
+        f.write("\n")
+    return len(lines)
+
+
+if __name__ == "__main__":
+    n = emit(sys.argv[1])
+    print(f"{n} lines")

@@ -1,0 +1,158 @@
+"""The forward's 256-row kernel (fwd_wide_kernel) forced on shapes the
+library would otherwise give to the 128-row kernel, against the oracle and
+against the 128-row kernel.
+
+swattn_prefill_fwd picks the 256-row kernel by itself only for large grids
+(1024 work items or more), which the config-sized tests cover; here
+SWATTN_FWD_KERNEL=wide / narrow forces one kernel or the other on the small
+shapes of test_gpu_parity (single and partial tiles, W = 1, W >= S,
+G = 1 / 5 / 8, B > 1, Skv != Sq), on packed sequences, on score ranges where
+the running maximum moves often (the rescale path) or keys keep rising along
+the sequence, and on the masked-tile edge cases (windows shorter than a
+64-key tile, rows whose window starts inside a tile).  Bars as in
+test_gpu_parity (O max-abs <= 2e-2, mean-abs <= 2e-3, LSE relative <= 1e-3;
+the NaN / -inf pattern of rows with no key must match the oracle's); the
+two kernels must agree to the same bars, and the 256-row kernel must be
+deterministic.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import routing as R
+from switchattentionkernels_amd import (build_switch_query_indices,
+                                        switch_gqa_prefill_varlen_forward, workloads)
+
+from test_gpu_parity import SMALL, _assert_close, _gpu_run, _mask, _oracle, _qkv
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _both(monkeypatch, q, k, v, m, w, **kw):
+    monkeypatch.setenv("SWATTN_FWD_KERNEL", "wide")
+    ow, lw, _, _ = _gpu_run(q, k, v, m, w, **kw)
+    monkeypatch.setenv("SWATTN_FWD_KERNEL", "narrow")
+    on, ln, _, _ = _gpu_run(q, k, v, m, w, **kw)
+    monkeypatch.delenv("SWATTN_FWD_KERNEL")
+    return ow, lw, on, ln
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p,skv", SMALL)
+def test_wide_small(monkeypatch, b, s, hq, hkv, w, p, skv):
+    q, k, v = _qkv(s * 7 + hq, b, s, hq, hkv, skv)
+    m = _mask(s, (b, s), p)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, w)
+    o_ref, lse_ref = _oracle(q, k, v, m, w)
+    tag = f"b{b} s{s} {hq}/{hkv} w{w} p{p} skv{skv}"
+    _assert_close(ow, lw, o_ref, lse_ref, tag="wide " + tag)
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow " + tag)
+
+
+@pytest.mark.parametrize("w", [1, 7, 40, 64, 65, 130])
+def test_wide_masked_tiles(monkeypatch, w):
+    """Windows from one key to just over two tiles: nearly every tile of a
+    local item is a masked tile, with the window start inside a half-tile,
+    on a tile edge or crossing the row block's keys."""
+    q, k, v = _qkv(31 + w, 1, 777, 8, 2)
+    m = _mask(31 + w, (1, 777), 0.3)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, w)
+    o_ref, lse_ref = _oracle(q, k, v, m, w)
+    _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide w{w}")
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow w{w}")
+
+
+@pytest.mark.parametrize("qk_scale,sm_scale", [(4.0, None), (1.0, 1.0), (0.05, None), (8.0, 1.0)])
+def test_wide_peaked_and_flat_softmax(monkeypatch, qk_scale, sm_scale):
+    """Nearly one-hot rows (the running maximum moves often, so the rescale
+    of O and l runs) and nearly uniform ones."""
+    gen = torch.Generator().manual_seed(21)
+    q, k, v = workloads.make_qkv(gen, 1, 700, 700, 8, 2, 128)
+    q, k = (q.float() * qk_scale).to(torch.bfloat16), (k.float() * qk_scale).to(torch.bfloat16)
+    m = _mask(21, (1, 700), 0.4)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 200, sm_scale=sm_scale)
+    o_ref, lse_ref = _oracle(q, k, v, m, 200, sm_scale=sm_scale)
+    _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide q,k x{qk_scale} sm_scale {sm_scale}")
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow x{qk_scale}")
+
+
+def test_wide_rising_scores(monkeypatch):
+    """Keys whose scores against every query rise along the sequence (each
+    key a growing multiple of one direction shared with the queries), so
+    that the running maximum of a full row moves in almost every half-tile,
+    by small and by large steps."""
+    s, hq, hkv = 900, 8, 2
+    gen = torch.Generator().manual_seed(5)
+    q, k, v = workloads.make_qkv(gen, 1, s, s, hq, hkv, 128)
+    d = torch.randn(128, generator=gen)
+    d = d / d.norm()
+    ramp = torch.linspace(0.0, 30.0, s).reshape(1, s, 1, 1)
+    jumps = (torch.arange(s) % 97 == 0).float().reshape(1, s, 1, 1) * 25.0
+    k = (k.float() * 0.3 + (ramp + jumps) * d).to(torch.bfloat16)
+    q = (q.float() * 0.3 + 2.0 * d).to(torch.bfloat16)
+    m = _mask(5, (1, s), 0.6)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 300)
+    o_ref, lse_ref = _oracle(q, k, v, m, 300)
+    _assert_close(ow, lw, o_ref, lse_ref, tag="wide rising scores")
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow rising scores")
+
+
+def test_wide_varlen(monkeypatch):
+    """Packed sequences of uneven lengths (some shorter than a tile, one
+    longer than the window) through the varlen entry point."""
+    cu = [0, 5, 64, 300, 301, 950, 1400]
+    t, hq, hkv, w = cu[-1], 16, 4, 256
+    gen = torch.Generator().manual_seed(8)
+    q, k, v = workloads.make_qkv(gen, 1, t, t, hq, hkv, 128)
+    mask = torch.rand((1, t), generator=gen) < 0.4
+    full, local = build_switch_query_indices(mask.to(DEV))
+    outs = {}
+    for kind in ("wide", "narrow"):
+        monkeypatch.setenv("SWATTN_FWD_KERNEL", kind)
+        outs[kind] = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
+                                                       cu, window_size=w)
+        torch.cuda.synchronize()
+    monkeypatch.delenv("SWATTN_FWD_KERNEL")
+    md = R.varlen_metadata(cu, cu, w)
+    f_o, l_o = R.compact(mask.numpy())
+    o_ref, lse_ref = oracle.routed_attention(q, k, v, f_o, l_o, metadata=md)
+    ow, lw = outs["wide"]
+    on, ln = outs["narrow"]
+    _assert_close(ow, lw, o_ref, lse_ref, tag="wide varlen")
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow varlen")
+
+
+def test_wide_deterministic_and_every_row_written(monkeypatch):
+    """Two calls give bit-identical O and LSE, and every routed row is
+    written (outputs pre-filled with NaN)."""
+    import ctypes
+    from switchattentionkernels_amd import _lib
+    monkeypatch.setenv("SWATTN_FWD_KERNEL", "wide")
+    b, s, hq, hkv, w = 2, 1500, 32, 8, 512
+    q, k, v = (x.to(DEV) for x in _qkv(77, b, s, hq, hkv))
+    m = _mask(77, (b, s), 0.35).to(DEV)
+    full, local = build_switch_query_indices(m)
+    L = _lib.lib()
+    ws_bytes = L.swattn_prefill_workspace_bytes(b, s, hkv, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    res = []
+    for _ in range(2):
+        out = torch.full_like(q, float("nan"))
+        lse = torch.full(q.shape[:3], float("nan"), device=DEV)
+        st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(), full.numel(),
+                                  local.data_ptr(), local.numel(), None, None, None, out.data_ptr(),
+                                  lse.data_ptr(), b, s, s, hq, hkv, 128, w,
+                                  ctypes.c_float(128 ** -0.5 * oracle.LOG2E), ws.data_ptr(), ws_bytes,
+                                  _lib.stream_handle(q.device))
+        assert st == 0, L.swattn_last_error()
+        torch.cuda.synchronize()
+        res.append((out, lse))
+    monkeypatch.delenv("SWATTN_FWD_KERNEL")
+    (o1, l1), (o2, l2) = res
+    assert not torch.isnan(o1).any() and not torch.isnan(l1).any()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    rows = np.arange(0, b * s, 13)
+    o_ref, lse_ref = _oracle(q.cpu(), k.cpu(), v.cpu(), m.cpu(), w, rows=rows)
+    _assert_close(o1, l1, o_ref, lse_ref, rows=rows, tag="wide b2 s1500 sampled")
