@@ -16,19 +16,28 @@ form is chosen per function, so it cannot keep O in AGPRs while S lives in
 VGPRs.  Written out here, O, Q^T and the LDS operands live in AGPRs (the
 matrix cores read and accumulate there directly) and S / P in VGPRs.
 
-Schedule.  One wave per SIMD issues everything in order, so the softmax
-must hide under the wave's own MFMAs.  Single-wave microbenchmarks on
-gfx950 show the rules the schedule follows: up to about five VALU
-instructions fit in the shadow of one 32x32x16 MFMA, a sixth costs a whole
-slot, and an exponential placed first behind an MFMA can stall the next
-one, so each MFMA slot takes at most one exponential and never as its
-first VALU instruction.  A 64-key tile has 64 exponentials and 64 MFMAs,
-so the exponentials must spread evenly over both GEMMs.  The online softmax
-therefore runs on 32-key halves of each tile (h = 0, 1; the running max
-moves at most per half): the scores of half 0 are final halfway through
-S = K Q^T, so its running max can be taken there and its exponentials can
-start as soon as P V of the previous tile does, which runs as two 16-MFMA
-halves.  Each step (tile j) is:
+Issue budget.  One wave per SIMD issues everything in order, and measured
+on gfx950 a wave issues about one instruction per five to six cycles, so
+an MFMA slot (32 cycles for a 32x32x16 bf16 MFMA) holds about five other
+instructions before the matrix core waits.  A step (one 64-key tile: 64
+MFMAs) has about 280 VALU instructions of softmax that cannot be avoided
+(two per exponential, the bf16 packing, the fp32 row sums, the running
+max), so everything else is kept off the path: the K and V^T rings have
+four slots each and the loop is unrolled four steps, so every LDS operand
+address is a base register plus an immediate offset; the buffer
+descriptors of the global -> LDS copies advance with four scalar
+instructions each; the two lanes of a row share one running-max update;
+LDS waits cover two operand reads where the second is old enough.  Rules
+from single-wave microbenchmarks: an exponential placed first behind an
+MFMA can stall the next one, so each MFMA slot takes at most one
+exponential and never as its first VALU instruction; a 64-key tile has 64
+exponentials and 64 MFMAs, so the exponentials spread over both GEMMs.
+
+Schedule.  The online softmax runs on 32-key halves of each tile (h = 0,
+1; the running max moves at most per half): the scores of half 0 are final
+halfway through S = K Q^T, so its running max can be taken there and its
+exponentials can start as soon as P V of the previous tile does, which runs
+as two 16-MFMA halves.  Each step (tile j) is:
 
   -- O, l *= 2^-e(j, 0) when some row's max moved in half 0 of tile j (rare) --
   A  (32 MFMAs, S(j+1) half 0 then half 1):  the exponentials of P(j)
@@ -38,8 +47,8 @@ halves.  Each step (tile j) is:
      half 0, packing of P(j) half 1, the running max of S(j+1) half 1;
   -- O, l *= 2^-e(j, 1) when some row's max moved in half 1 of tile j (rare) --
   B2 (16 MFMAs, P(j) V(j) half 1):  the last 16 exponentials of S(j+1)
-     half 0, row sums of P(j) half 1; the ring slots move on, and the next
-     step's first K operands are read (before its barrier).
+     half 0, row sums of P(j) half 1; then the next step's first K and V^T
+     operands are read (before its barrier).
 
 Work a block cannot fit moves on to the next one (never past a rescale it
 must precede).  The running max is kept as n = -m c; a half's max x moves
@@ -56,16 +65,17 @@ dependent ones (the rules at the end, checked over the control-flow graph
 so that every path is covered).
 
 Register map (per lane; "rb" = row block 0/1 of the wave's 64 rows, "h" =
-32-key half of a 64-key tile, "db" = 32-wide block of head_dim):
+32-key half of a 64-key tile, "db" = 32-wide block of head_dim; "combined"
+values hold row block 0 in lanes 0-31 and row block 1 in lanes 32-63):
   a[0:127]    O^T accumulators, block (db, rb) at a[32 db + 16 rb]
   a[128:191]  Q^T operands, k-step kk (16 of head_dim), rb at a[128 + 8 kk + 4 rb]
   a[192:223]  K operands, eight sets (one per (h, kk) read)
   a[224:247]  V^T operands, six sets
   v[0:63], v[64:127]   S tiles (ping-pong), (rb, h) at +32 rb + 16 h
   v[128:159]  P^T operands (bf16), k-step s2 (16 keys), rb at v[128 + 8 s2 + 4 rb]
-  v[160:167]  K operand LDS addresses per kk; v[168:171] V^T per s2
-  v[172:223]  row state and temporaries
-  v[224:255]  left to the compiler (the asm's inputs)
+  v[160:167]  K operand LDS addresses (slot 0) per kk; v[168:171] V^T per s2
+  v[172:215]  row state and temporaries
+  v[216:255]  left to the compiler (the asm's inputs)
 """
 
 from __future__ import annotations
@@ -81,40 +91,36 @@ K_SETS, V_SETS = 8, 6      # LDS operand sets in flight
 S_V = (0, 64)
 PK_V = 128
 KOFF_V, VOFF_V = 160, 168
-V_L = 174                            # [rb] this lane's partial row sum
-V_AL = 176                           # rescale exponent [tile parity][h][rb] at 176 + 4 par + 2 h + rb
-V_NMC = 184                          # -m c after half h [h][rb] at 184 + 2 h + rb
-V_SPAN, V_KSR = 188, 190             # [rb]
-V_MXA, V_MXB = 192, 194              # [rb]
-V_NSENT = 199                        # -c times the max sentinel
-V_NINF = 200                         # -inf
-V_RS = 201                           # 201..208 rescale temporaries
-V_RA = 209                           # [rb] the exponent the rescale routine applies
-V_D, V_MT = 211, 213                 # [rb] running-max temporaries (V_D doubles as the mask's lo)
-V_MK = 217                           # 217..220 mask temporaries
-V_T = 188                            # epilogue temporaries (loop registers free by then)
+V_L = 172                            # [rb] this lane's partial row sum
+V_AL = 174                           # rescale exponent (combined) [tile parity][h] at 174 + 2 par + h
+V_NMC = 178                          # n = -m c after half h, [h][rb] at 178 + 2 h + rb
+V_NMCC = 182                         # n (combined) after the last half taken
+V_SPAN, V_KSR = 183, 185             # [rb] row key range: length, start - 4 hh
+V_MXA, V_MXB = 187, 189              # [rb] max-chain accumulators
+V_M, V_D, V_MT = 191, 192, 193       # combined half max and running-max temporaries
+V_NSENT = 194                        # n of the max sentinel
+V_NINF = 195                         # -inf
+V_RS = 196                           # 196..203 rescale temporaries
+V_RA = 204                           # [rb] the exponent the rescale routine applies
+V_MK = 206                           # 206..209 mask temporaries
+V_LO = 210                           # [rb] mask: row start - 4 hh - first key of the tile
+V_T = 188                            # epilogue temporaries (the loop's registers are free by then)
 V_EPI = 209                          # 209..215 epilogue lane addresses
-V_LIMIT = 224                        # first VGPR left to the compiler
+V_LIMIT = 216                        # first VGPR left to the compiler
 
 # clobbered SGPRs
 S_RET = 52                  # return address of the rescale routine (2)
 S_FLAG = 54                 # rescale flags [tile parity][h] (2 each) at 54 + 4 par + 2 h
-S_T3, S_T4 = 62, 63
-S_WV, S_MK, S_MV = 64, 65, 66   # V^T DMA slot offset; M0 bases of this step's K / V^T DMAs
-S_T2 = 67
-S_WK, S_RK_OLD = 68, 69     # K DMA slot offset; the K read slot offset the address registers hold
-S_R, S_N = 70, 71           # step index r, tile count
-S_KPTR, S_KRL = 72, 74      # running K tile pointer (2), rows left (next K tile to stage)
-S_RK = 75                   # LDS offset of the K slot this step reads
-S_KRS, S_VRS = 76, 80       # K / V^T buffer descriptors (4 each)
-S_VPTR = 84                 # running V^T tile pointer (2)
-S_T0, S_T1 = 86, 87
-S_PAIRS = (88, 90, 92, 94)  # VALU compare results (2 each)
-S_MASK = 96                 # nonzero: this step's S(j+1) needs the range mask
-S_KEY0 = 98
-S_EIGHT, S_SENT = 99, 100   # 8.0 and the -2^30 max sentinel
-S_RV = 101                  # LDS offset (inside the V^T ring) of the V^T slot this step reads
-S_FIRST, S_LASTC = 52, 101  # clobbered range
+S_T0, S_T1 = 62, 63
+S_R1 = 64                   # r + 1 for step r (the tile whose scores the step computes)
+S_N = 65                    # tile count
+S_SPAN = 66                 # it1 - it0: tiles r + 1 - it0 below it need no range mask
+S_KEY0 = 67                 # first key of tile r + 1 (masked steps)
+S_KBYTES, S_VBYTES = 68, 69  # bytes from the current K / V^T descriptor base to the item's end
+S_KRS, S_VRS = 72, 76       # K / V^T buffer descriptors (4 each)
+S_PAIRS = (80, 82, 84, 86)  # VALU compare results (2 each)
+S_EIGHT, S_SENT = 88, 89    # 8.0 and the -2^30 max sentinel
+S_FIRST, S_LASTC = 52, 89   # clobbered range
 
 SENTINEL_BITS = 0xCE800000   # -2^30 as fp32 (V:174)
 NEG_INF_BITS = 0xFF800000
@@ -122,12 +128,12 @@ EIGHT_BITS = 0x41000000
 RSRC_WORD3 = 0x00020000
 
 TILE_BYTES = 16384           # one K or V^T tile in LDS
-K_SLOTS = 4                  # K(j) staged three steps before it is read (so its first
-                             # operands can be read before the step's barrier)
-V_SLOTS = 3                  # V^T(j) staged two steps before it is read
+K_SLOTS = V_SLOTS = 4        # tile j+1's K and tile j's V^T are staged three steps before step j
 V_RING = K_SLOTS * TILE_BYTES  # byte offset of the V^T ring
 LDS_BYTES = V_RING + V_SLOTS * TILE_BYTES
 EPI_REGION = 32 * 272 + 128  # per-wave O staging for 32 rows + their offsets
+N_PRE_K, N_PRE_V = 4, 2      # operand reads of the next step issued before its barrier
+PRO_LATE = 16                # prologue DMAs the pre step does not wait for
 
 # ---------------------------------------------------------------------------
 # instructions
@@ -225,11 +231,11 @@ def kop(h, kk):
     return KOP_A + 4 * ((8 * h + kk) % K_SETS)
 
 
-def k_read(h, kk):
-    """K operand of k-step kk for the 32 keys of half h, from the K slot the
-    address registers point at."""
+def k_read(h, kk, slot):
+    """K operand of k-step kk for the 32 keys of half h of the tile in K
+    slot `slot`."""
     dst = kop(h, kk)
-    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(KOFF_V + kk)} offset:{h * 8192}",
+    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(KOFF_V + kk)} offset:{slot * TILE_BYTES + h * 8192}",
                "lds", {f"v{KOFF_V + kk}"}, regs("a", dst, 4), lgkm=True)
 
 
@@ -242,9 +248,11 @@ def vop(s2, db):
     return VOP_A + 4 * ((4 * s2 + db) % V_SETS)
 
 
-def v_read(s2, db):
+def v_read(s2, db, slot):
+    """V^T operand (keys 16 s2.., head_dim block db) of the tile in V^T slot
+    `slot` (the address registers include the ring's offset)."""
     dst = vop(s2, db)
-    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(VOFF_V + s2)} offset:{db * 4096}",
+    return Ins(f"ds_read_b128 {areg(dst, 4)}, {vreg(VOFF_V + s2)} offset:{slot * TILE_BYTES + db * 4096}",
                "lds", {f"v{VOFF_V + s2}"}, regs("a", dst, 4), lgkm=True)
 
 
@@ -256,50 +264,29 @@ def pv_mfmas(s2, db):
 V_SEQ = [(s2, db) for s2 in range(4) for db in range(4)]
 
 
-def dma(kind, i):
-    """One global -> LDS load of this wave's share of a K (kind 'k') or V^T
-    tile into the slot whose M0 base this step set up."""
+def dma(kind, i, slot):
+    """One global -> LDS load of this wave's quarter of a K (kind 'k') or
+    V^T tile into slot `slot` of its ring."""
     rs = S_KRS if kind == "k" else S_VRS
-    mb = S_MK if kind == "k" else S_MV
+    base = slot * TILE_BYTES + (0 if kind == "k" else V_RING) + i * 1024
     off = s_in(f"{kind}dma{i}")
-    return [salu(f"s_add_u32 m0, {sreg(mb)}, {i * 1024}", wr={"m0"}),
+    return [salu(f"s_add_u32 m0, {s_in('ldsw')}, {base}", wr={"m0"}),
             Ins(f"buffer_load_dwordx4 {off}, {sreg(rs, 4)}, 0 offen lds", "dma",
                 regs("s", rs, 4) | {"m0"}, set(), vm=True)]
 
 
-def k_desc():
-    """K descriptor for tile r + 4 (empty past the last tile or the keys),
-    then advance the running pointer and row count by one tile."""
-    t0, t1 = sreg(S_T0), sreg(S_T1)
-    return [
-        salu(f"s_min_i32 {t0}, {sreg(S_KRL)}, {s_in('kmaxrows')}"),
-        salu(f"s_max_i32 {t0}, {t0}, 0"),
-        salu(f"s_mul_i32 {t0}, {t0}, {s_in('krowbytes')}"),
-        salu(f"s_add_u32 {t1}, {sreg(S_R)}, {K_SLOTS}"),
-        salu(f"s_cmp_lt_i32 {t1}, {sreg(S_N)}"),
-        salu(f"s_cselect_b32 {sreg(S_KRS + 2)}, {t0}, 0"),
-        salu(f"s_mov_b32 {sreg(S_KRS)}, {sreg(S_KPTR)}"),
-        salu(f"s_and_b32 {sreg(S_KRS + 1)}, {sreg(S_KPTR + 1)}, 0xffff"),
-        salu(f"s_mov_b32 {sreg(S_KRS + 3)}, {RSRC_WORD3:#x}"),
-        salu(f"s_add_u32 {sreg(S_KPTR)}, {sreg(S_KPTR)}, {s_in('ktilebytes')}"),
-        salu(f"s_addc_u32 {sreg(S_KPTR + 1)}, {sreg(S_KPTR + 1)}, 0"),
-        salu(f"s_sub_i32 {sreg(S_KRL)}, {sreg(S_KRL)}, 64"),
-    ]
-
-
-def v_desc():
-    """V^T descriptor for tile r + 2 (empty past the last tile), then advance."""
-    t1 = sreg(S_T1)
-    return [
-        salu(f"s_add_u32 {t1}, {sreg(S_R)}, 2"),
-        salu(f"s_cmp_lt_i32 {t1}, {sreg(S_N)}"),
-        salu(f"s_cselect_b32 {sreg(S_VRS + 2)}, {TILE_BYTES}, 0"),
-        salu(f"s_mov_b32 {sreg(S_VRS)}, {sreg(S_VPTR)}"),
-        salu(f"s_and_b32 {sreg(S_VRS + 1)}, {sreg(S_VPTR + 1)}, 0xffff"),
-        salu(f"s_mov_b32 {sreg(S_VRS + 3)}, {RSRC_WORD3:#x}"),
-        salu(f"s_add_u32 {sreg(S_VPTR)}, {sreg(S_VPTR)}, {TILE_BYTES}"),
-        salu(f"s_addc_u32 {sreg(S_VPTR + 1)}, {sreg(S_VPTR + 1)}, 0"),
-    ]
+def desc_advance(kind):
+    """Move a descriptor on to the next tile: base += tile, the bytes left to
+    the item's end shrink by a tile, and the record count is what is left
+    (none past the item's last tile, part of the keys' last tile)."""
+    if kind == "k":
+        rs, nb, step = S_KRS, S_KBYTES, s_in("ktilebytes")
+    else:
+        rs, nb, step = S_VRS, S_VBYTES, str(TILE_BYTES)
+    return [salu(f"s_add_u32 {sreg(rs)}, {sreg(rs)}, {step}"),
+            salu(f"s_addc_u32 {sreg(rs + 1)}, {sreg(rs + 1)}, 0"),
+            salu(f"s_sub_i32 {sreg(nb)}, {sreg(nb)}, {step}"),
+            salu(f"s_max_i32 {sreg(rs + 2)}, {sreg(nb)}, 0")]
 
 
 def half_elems(s, h):
@@ -367,43 +354,16 @@ def sums(s, h):
     return out
 
 
-def mask(s, h):
-    """Scores of half h outside each row's [start, end) set to -inf.
-    Register r of the half is key 32 h + 8 (r >> 2) + 4 hh + (r & 3) of the
-    tile; the row bounds were shifted by 4 hh, so it is legal iff
-    (off - lo) < span, unsigned, with lo = start - 4 hh - key0."""
-    out = []
-    for rb in range(2):
-        out.append(valu(f"v_subrev_u32 {vreg(V_D + rb)}, {sreg(S_KEY0)}, {vreg(V_KSR + rb)}",
-                        {f"v{V_KSR + rb}", f"s{S_KEY0}"}, {f"v{V_D + rb}"}))
-    elems = [(rb, r) for rb in range(2) for r in range(16)]
-    for g in range(0, len(elems), 4):
-        grp = elems[g:g + 4]
-        for k, (rb, r) in enumerate(grp):
-            off = 32 * h + 8 * (r >> 2) + (r & 3)
-            out.append(valu(f"v_sub_u32 {vreg(V_MK + k)}, {off}, {vreg(V_D + rb)}", {f"v{V_D + rb}"},
-                            {f"v{V_MK + k}"}))
-        for k, (rb, r) in enumerate(grp):
-            p = S_PAIRS[k]
-            out.append(valu(f"v_cmp_gt_u32_e64 {sreg(p, 2)}, {vreg(V_SPAN + rb)}, {vreg(V_MK + k)}",
-                            {f"v{V_SPAN + rb}", f"v{V_MK + k}"}, {f"s{p}", f"s{p + 1}"}))
-        for k, (rb, r) in enumerate(grp):
-            x = s + 32 * rb + 16 * h + r
-            p = S_PAIRS[k]
-            out.append(valu(f"v_cndmask_b32_e64 {vreg(x)}, {vreg(V_NINF)}, {vreg(x)}, {sreg(p, 2)}",
-                            {f"v{x}", f"v{V_NINF}"}, {f"v{x}"}, mask_rd={f"s{p}", f"s{p + 1}"}))
-    return out
-
-
 def running_max(s, h, par):
-    """Row max of half h of S, then the running max: with n = -m c of the
-    running max m (kept instead of m) and d = x c + n for the half's max x,
-    m moves to x only when d > 8 (the half's exponentials then stay below
-    2^8 without it); then n = -x c, and the half's rescale exponent is d
-    (O and l are multiplied by 2^-d), else 0.  The flag of (tile parity par,
-    h) is set when some row of the wave moved from a finite max (a row still
-    at the sentinel has O = 0 and l = 0).  Both row blocks' chains are
-    interleaved; all of it is marked urgent for the scheduler."""
+    """Row max of half h of S (per lane over its 16 keys, then the two lanes
+    of each row with one lane swap that leaves the combined max: row block
+    0 in lanes 0-31, row block 1 in lanes 32-63), then one running-max
+    update for both row blocks: d = x c + n, the max moves when d > 8 (n
+    becomes -x c and the rescale exponent is d, else 0), and the flag of
+    (tile parity par, h) is set when some row moved from a finite max (a
+    row still at the sentinel has O = 0 and l = 0); then n goes to each
+    row block's lanes for the exponentials.  Marked urgent for the
+    scheduler."""
     chains = []
     for rb in range(2):
         b = s + 32 * rb + 16 * h
@@ -417,40 +377,65 @@ def running_max(s, h, par):
                           {f"v{acc}", f"v{b + i}", f"v{b + i + 1}"}, {f"v{acc}"}))
             acc = xb if acc == xa else xa
         c.append(valu(f"v_max_f32 {vreg(xa)}, {vreg(xa)}, {vreg(xb)}", {f"v{xa}", f"v{xb}"}, {f"v{xa}"}))
-        c += swap_combine(xa, xb, "v_max_f32")
         chains.append(c)
     out = []
     for a, b in zip(chains[0], chains[1]):
         out += [a, b]
+    x0, x1 = V_MXA, V_MXA + 1
+    pm, pq = S_PAIRS[0], S_PAIRS[1]
     flag = S_FLAG + 4 * par + 2 * h
-    upd = []
-    for rb in range(2):
-        xa = V_MXA + rb
-        d, t = V_D + rb, V_MT + rb
-        pm, pq = S_PAIRS[2 * rb], S_PAIRS[2 * rb + 1]
-        nprev, nmc = V_NMC + 2 * (1 - h) + rb, V_NMC + 2 * h + rb
-        al = V_AL + 4 * par + 2 * h + rb
-        upd.append([
-            valu(f"v_fma_f32 {vreg(d)}, {vreg(xa)}, {s_in('c')}, {vreg(nprev)}", {f"v{xa}", f"v{nprev}"},
-                 {f"v{d}"}),
-            valu(f"v_cmp_neq_f32_e64 {sreg(pq, 2)}, {vreg(V_NSENT)}, {vreg(nprev)}",
-                 {f"v{V_NSENT}", f"v{nprev}"}, {f"s{pq}", f"s{pq + 1}"}),
-            valu(f"v_mul_f32 {vreg(t)}, {s_in('negc')}, {vreg(xa)}", {f"v{xa}"}, {f"v{t}"}),
-            valu(f"v_cmp_lt_f32_e64 {sreg(pm, 2)}, {sreg(S_EIGHT)}, {vreg(d)}", {f"v{d}", f"s{S_EIGHT}"},
-                 {f"s{pm}", f"s{pm + 1}"}),
-            valu(f"v_cndmask_b32_e64 {vreg(al)}, 0, {vreg(d)}, {sreg(pm, 2)}", {f"v{d}"}, {f"v{al}"},
-                 mask_rd={f"s{pm}", f"s{pm + 1}"}),
-            valu(f"v_cndmask_b32_e64 {vreg(nmc)}, {vreg(nprev)}, {vreg(t)}, {sreg(pm, 2)}",
-                 {f"v{nprev}", f"v{t}"}, {f"v{nmc}"}, mask_rd={f"s{pm}", f"s{pm + 1}"}),
-            salu(f"s_and_b64 {sreg(pq, 2)}, {sreg(pq, 2)}, {sreg(pm, 2)}", {f"s{pq}", f"s{pm}", f"s{pm + 1}"},
-                 {f"s{pq}", f"s{pq + 1}"}),
-        ])
-    for a, b in zip(upd[0], upd[1]):
-        out += [a, b]
-    out.append(salu(f"s_or_b64 {sreg(flag, 2)}, {sreg(S_PAIRS[1], 2)}, {sreg(S_PAIRS[3], 2)}",
-                    {f"s{S_PAIRS[1]}", f"s{S_PAIRS[3]}"}, {f"s{flag}", f"s{flag + 1}"}))
+    al = V_AL + 2 * par + h
+    n0, n1 = V_NMC + 2 * h, V_NMC + 2 * h + 1
+    out += [
+        Ins(f"v_permlane32_swap_b32 {vreg(x0)}, {vreg(x1)}", "perm", {f"v{x0}", f"v{x1}"}, {f"v{x0}", f"v{x1}"}),
+        valu(f"v_max_f32 {vreg(V_M)}, {vreg(x0)}, {vreg(x1)}", {f"v{x0}", f"v{x1}"}, {f"v{V_M}"}),
+        valu(f"v_fma_f32 {vreg(V_D)}, {vreg(V_M)}, {s_in('c')}, {vreg(V_NMCC)}", {f"v{V_M}", f"v{V_NMCC}"},
+             {f"v{V_D}"}),
+        valu(f"v_cmp_neq_f32_e64 {sreg(pq, 2)}, {vreg(V_NSENT)}, {vreg(V_NMCC)}", {f"v{V_NSENT}", f"v{V_NMCC}"},
+             {f"s{pq}", f"s{pq + 1}"}),
+        valu(f"v_mul_f32 {vreg(V_MT)}, {s_in('negc')}, {vreg(V_M)}", {f"v{V_M}"}, {f"v{V_MT}"}),
+        valu(f"v_cmp_lt_f32_e64 {sreg(pm, 2)}, {sreg(S_EIGHT)}, {vreg(V_D)}", {f"v{V_D}", f"s{S_EIGHT}"},
+             {f"s{pm}", f"s{pm + 1}"}),
+        valu(f"v_cndmask_b32_e64 {vreg(al)}, 0, {vreg(V_D)}, {sreg(pm, 2)}", {f"v{V_D}"}, {f"v{al}"},
+             mask_rd={f"s{pm}", f"s{pm + 1}"}),
+        valu(f"v_cndmask_b32_e64 {vreg(V_NMCC)}, {vreg(V_NMCC)}, {vreg(V_MT)}, {sreg(pm, 2)}",
+             {f"v{V_NMCC}", f"v{V_MT}"}, {f"v{V_NMCC}"}, mask_rd={f"s{pm}", f"s{pm + 1}"}),
+        salu(f"s_and_b64 {sreg(flag, 2)}, {sreg(pq, 2)}, {sreg(pm, 2)}",
+             {f"s{pq}", f"s{pq + 1}", f"s{pm}", f"s{pm + 1}"}, {f"s{flag}", f"s{flag + 1}"}),
+        valu(f"v_mov_b32 {vreg(n0)}, {vreg(V_NMCC)}", {f"v{V_NMCC}"}, {f"v{n0}"}),
+        valu(f"v_mov_b32 {vreg(n1)}, {vreg(V_NMCC)}", {f"v{V_NMCC}"}, {f"v{n1}"}),
+        Ins(f"v_permlane32_swap_b32 {vreg(n0)}, {vreg(n1)}", "perm", {f"v{n0}", f"v{n1}"}, {f"v{n0}", f"v{n1}"}),
+    ]
     for x in out:
         x.urgent = True
+    return out
+
+
+def mask(s, h):
+    """Scores of half h outside each row's [start, end) set to -inf.
+    Register r of the half is key 32 h + 8 (r >> 2) + 4 hh + (r & 3) of the
+    tile; the row bounds were shifted by 4 hh, so it is legal iff
+    (off - lo) < span, unsigned, with lo = start - 4 hh - key0."""
+    out = []
+    for rb in range(2):
+        out.append(valu(f"v_subrev_u32 {vreg(V_LO + rb)}, {sreg(S_KEY0)}, {vreg(V_KSR + rb)}",
+                        {f"v{V_KSR + rb}", f"s{S_KEY0}"}, {f"v{V_LO + rb}"}))
+    elems = [(rb, r) for rb in range(2) for r in range(16)]
+    for g in range(0, len(elems), 4):
+        grp = elems[g:g + 4]
+        for k, (rb, r) in enumerate(grp):
+            off = 32 * h + 8 * (r >> 2) + (r & 3)
+            out.append(valu(f"v_sub_u32 {vreg(V_MK + k)}, {off}, {vreg(V_LO + rb)}", {f"v{V_LO + rb}"},
+                            {f"v{V_MK + k}"}))
+        for k, (rb, r) in enumerate(grp):
+            p = S_PAIRS[k]
+            out.append(valu(f"v_cmp_gt_u32_e64 {sreg(p, 2)}, {vreg(V_SPAN + rb)}, {vreg(V_MK + k)}",
+                            {f"v{V_SPAN + rb}", f"v{V_MK + k}"}, {f"s{p}", f"s{p + 1}"}))
+        for k, (rb, r) in enumerate(grp):
+            x = s + 32 * rb + 16 * h + r
+            p = S_PAIRS[k]
+            out.append(valu(f"v_cndmask_b32_e64 {vreg(x)}, {vreg(V_NINF)}, {vreg(x)}, {sreg(p, 2)}",
+                            {f"v{x}", f"v{V_NINF}"}, {f"v{x}"}, mask_rd={f"s{p}", f"s{p + 1}"}))
     return out
 
 
@@ -482,11 +467,11 @@ def rescale_routine():
     return out
 
 
-SLOT_CYCLES = 32
-VALU_ISSUE = 5
-LAT = {"valu": 8, "trans": 24, "perm": 12}
-SLOT_CAP = 5
-MF_LAT = 40          # cycles from an MFMA's issue to a VALU read of its result
+# ---------------------------------------------------------------------------
+# list scheduling of a block
+# ---------------------------------------------------------------------------
+
+MF_DIST = 12          # instructions between an MFMA and a VALU read of its result
 
 
 def _conflict(a, b):
@@ -495,20 +480,36 @@ def _conflict(a, b):
     return bool(a.wr & (b.rd | b.wr | b.mask_rd) or b.wr & (a.rd | a.mask_rd))
 
 
-def schedule(mfmas, valu_list, side=None, lead_cap=4, carry=False, n_carried=0):
+def _dist(a, b):
+    """Instructions b must trail a by (a before b, conflicting): the
+    wait states gfx950 needs between them, so that no s_nop is needed."""
+    if a.trans and a.wr & (b.rd | b.mask_rd):
+        return 3
+    if b.kind == "perm" and a.wr & b.rd:
+        return 3
+    if any(r.startswith("s") for r in a.wr & b.mask_rd) and a.kind != "salu":
+        return 3
+    return 1
+
+
+def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
     """Order one block: the MFMAs in their given order, side(i) (LDS reads,
-    DMAs) emitted before MFMA i and side(len) after the last, and the VALU /
-    SALU list (in a valid program order) placed into the MFMA slots by a
-    greedy list scheduler with a small cycle model.  Slot s is the gap after
-    MFMA s - 1 (slot 0: before the first).  VALU work that touches an MFMA's
-    registers stays after that MFMA (reading its result about one MFMA
-    later), and work that touches a side instruction's registers stays after
-    it; the first n_carried items come from the previous block instead and
-    go before any MFMA of this block whose registers they touch.  Each slot
-    takes at most SLOT_CAP VALU instructions and one exponential, never
-    first; exponentials, then urgent work, go first among what is ready.
-    With carry, what does not fit is returned for the next block instead of
-    being issued after the last MFMA."""
+    DMAs, descriptor updates) right before MFMA i and side(len) after the
+    last, and the VALU / SALU list (in a valid program order) spread over
+    the gaps between MFMAs (slot s: before MFMA s) so that every gap issues
+    about the same number of instructions, side work included (a wave
+    issues about one instruction per five to six cycles, so the gaps are
+    where the MFMAs wait).  Work that touches an MFMA's registers stays
+    after that MFMA (MF_DIST instructions after it for a read of its
+    result), and work that touches a side instruction's registers stays
+    after it; the first n_carried items come from the previous block
+    instead and go before any MFMA of this block whose registers they
+    touch.  Dependent instructions keep the distance gfx950 needs between
+    them.  Each gap takes at most one exponential, never as its first
+    instruction; exponentials (and the FMAs that feed them), then urgent
+    work, go first among what is ready.  With carry, what does not fit is
+    returned for the next block instead of being issued after the last
+    MFMA."""
     n = len(valu_list)
     nm = len(mfmas)
     sides = [side(i) if side is not None else [] for i in range(nm + 1)]
@@ -536,7 +537,7 @@ def schedule(mfmas, valu_list, side=None, lead_cap=4, carry=False, n_carried=0):
         for i in range(nm):
             if any(_conflict(x, v) for x in sides[i]):
                 assert j >= n_carried or deadline[j] == nm
-                min_slot[j] = max(min_slot[j], i + 1 if i > 0 else 0)
+                min_slot[j] = max(min_slot[j], i + 1)
         if any(_conflict(x, v) for x in sides[nm]):
             assert not carry, "a carried instruction conflicts with the block's last side work"
     for j in range(n):
@@ -544,153 +545,157 @@ def schedule(mfmas, valu_list, side=None, lead_cap=4, carry=False, n_carried=0):
             deadline[k] = min(deadline[k], deadline[j])
     issued = [False] * n
     npred = [len(p) for p in preds]
-    ready_at = [0] * n
+    ready = [0] * n
     out = []
-    state = {"t": 0, "done": 0, "fed": 0}
+    st = {"pos": 0, "fed": 0, "done": 0}
 
-    def pick(slot, slot_end, first, n_exp):
-        best = None
-        for j in range(n):
-            if issued[j] or npred[j] or min_slot[j] > slot:
-                continue
-            v = valu_list[j]
-            if v.trans and (first or n_exp >= 1):
-                continue
-            start = max(state["t"], ready_at[j])
-            if start + VALU_ISSUE > slot_end:
-                continue
-            lead = v.trans or (v.feeds_trans and state["fed"] < 2)
-            key = (start, not lead, not v.urgent, j)
-            if best is None or key < best[1]:
-                best = (j, key)
-        return None if best is None else (best[0], best[1][0])
+    def put(x):
+        out.append(x)
+        st["pos"] += 1
 
-    def issue(j, start):
+    def issue(j):
         issued[j] = True
         v = valu_list[j]
-        out.append(v)
-        state["t"] = start + (VALU_ISSUE if v.kind != "salu" else 1)
+        put(v)
         if v.feeds_trans:
-            state["fed"] += 1
-        if v.trans and state["fed"]:
-            state["fed"] -= 1
-        lat = LAT["trans"] if v.trans else LAT.get(v.kind, LAT["valu"])
+            st["fed"] += 1
+        if v.trans and st["fed"]:
+            st["fed"] -= 1
         for k in succs[j]:
             npred[k] -= 1
-            ready_at[k] = max(ready_at[k], start + lat)
-        state["done"] += 1
+            ready[k] = max(ready[k], st["pos"] - 1 + _dist(v, valu_list[k]))
+        st["done"] += 1
 
-    def fill(slot, slot_end, cap):
+    def pick(slot, first, n_exp, relax=False):
+        best = None
+        for j in range(n):
+            if issued[j] or npred[j] or min_slot[j] > slot or (ready[j] > st["pos"] and not relax):
+                continue
+            v = valu_list[j]
+            if v.trans and (first or n_exp >= 1) and not relax:
+                continue
+            lead = v.trans or (v.feeds_trans and st["fed"] < 2)
+            key = (not lead, not v.urgent, j)
+            if best is None or key < best[1]:
+                best = (j, key)
+        return None if best is None else best[0]
+
+    def fill(slot, cap, drain=False):
         first, n_exp, cnt = True, 0, 0
         while cnt < cap:
-            b = pick(slot, slot_end, first, n_exp)
-            if b is None:
+            j = pick(slot, first, n_exp)
+            if j is None and drain:
+                j = pick(slot, first, n_exp, relax=True)
+            if j is None:
                 break
-            j, start = b
-            issue(j, start)
+            issue(j)
             first = False
             n_exp += valu_list[j].trans
-            cnt += valu_list[j].kind != "salu"
+            cnt += 1
 
     def force(i):
         """Issue, in list order, the carried work MFMA i must follow."""
         for j in range(n):
             if not issued[j] and deadline[j] <= i:
                 assert npred[j] == 0
-                issue(j, max(state["t"], ready_at[j]))
+                issue(j)
 
-    out += sides[0]
-    fill(0, state["t"] + SLOT_CYCLES, lead_cap if mfmas else n)
-    for i, m in enumerate(mfmas):
-        if i > 0:
-            out += sides[i]
-        force(i)
-        out.append(m)
-        t0 = max(state["t"], i * SLOT_CYCLES)
-        for j in mf_users[i]:
-            ready_at[j] = max(ready_at[j], t0 + MF_LAT)
-        state["t"] = t0 + 2
-        remaining = n - state["done"]
-        slots_left = nm - i
-        cap = min(SLOT_CAP + 1, max(1, -(-remaining // slots_left)))
-        fill(i + 1, t0 + SLOT_CYCLES, cap)
-    left = []
-    if carry and nm:
-        left = [valu_list[j] for j in range(n) if not issued[j]]
-    else:
-        while state["done"] < n:
-            b = pick(nm + 1, 1 << 30, False, 0)
-            assert b is not None
-            issue(*b)
-    out += sides[nm]
+    side_left = sum(len(s) for s in sides)
+    for i in range(nm + 1):
+        remaining = n - st["done"] + side_left
+        if i == 0:
+            cap = lead_cap if nm else n
+        elif i == nm and not carry:
+            cap = n
+        else:
+            cap = max(1, -(-remaining // (nm + 1 - i)) - len(sides[i]))
+        # an M0 write goes ahead of the slot's VALU work: the LDS DMA after
+        # it then needs no s_nop
+        early = [x for x in sides[i] if "m0" in x.wr]
+        assert len(early) <= 1
+        for x in early:
+            put(x)
+        fill(i, cap, drain=(i == nm and not carry) or not nm)
+        for x in sides[i]:
+            if x not in early:
+                put(x)
+        side_left -= len(sides[i])
+        if i < nm:
+            force(i)
+            put(mfmas[i])
+            for j in mf_users[i]:
+                ready[j] = max(ready[j], st["pos"] - 1 + MF_DIST)
+    left = [valu_list[j] for j in range(n) if not issued[j]]
+    if not carry or not nm:
+        assert not left, "unscheduled work"
     return out, left
 
 
 # ---------------------------------------------------------------------------
 # blocks of a step
 # ---------------------------------------------------------------------------
+# Step r (phase q = r mod 4) computes S(r+1) from K(r+1) in K slot (q+1)%4
+# and P(r) V(r) from V^T(r) in V^T slot q; it stages K(r+4) into K slot q
+# (read by step r-1) and V^T(r+3) into V^T slot (q+3)%4 (read by step r-1),
+# and at its end reads the first operands of K(r+2) and V^T(r+1).
 
-def block_a(par, kind, masked):
+def block_a(q, kind, masked):
     """S(j+1) = K(j+1) Q^T in 32 MFMAs (half 0, then half 1) while P(j)
     half 1 is exponentiated, P(j) half 0 packed and summed, and S(j+1)
     half 0's running max taken.  kind 'pre' (tile 0's S only), 'full',
     'last' (no S(j+1)).  Returns (instructions, leftover VALU)."""
+    par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
     pn = 1 - par           # parity of tile j + 1
+    ks = (q + 1) % 4
     out = []
-    dmas = []
-    if kind != "last":
-        out += k_desc()
-        dmas = [dma("k", i) for i in range(4)]
     vl = []
     if kind != "pre":
         vl += exps(scur, 1, 0, 32) + packs(scur, 0) + sums(scur, 0)
     if kind != "last":
         if masked:
+            out += [salu(f"s_lshl_b32 {sreg(S_KEY0)}, {sreg(S_R1)}, 6"),
+                    salu(f"s_add_u32 {sreg(S_KEY0)}, {sreg(S_KEY0)}, {s_in('key0')}")]
             vl += mask(snxt, 0)
         vl += running_max(snxt, 0, pn)
     if kind == "last":
-        out += [v_read(*x) for x in V_SEQ[:V_SETS - 1]]
+        out += [v_read(*x, q) for x in V_SEQ[N_PRE_V:V_SETS - 1]]
         o, _ = schedule([], vl)
         return out + o, []
+    dmas = [dma("k", i, q) for i in range(4)]
     mf = []
     for h in range(2):
         for kk in range(8):
             mf += qk_mfmas(snxt, h, kk)
     reads = [(h, kk) for h in range(2) for kk in range(8)]
-    pre = 4 if kind != "pre" else 0     # K operands read before the barrier
+    pre = N_PRE_K if kind != "pre" else 0     # K operands read before the barrier
+    vre = [V_SEQ[k] for k in range(N_PRE_V, V_SETS - 1)] if kind == "full" else []
 
     def side(i):
         r = []
         if i == 0:
-            r += [k_read(*x) for x in reads[pre:6]]
-        q = i // 2
-        if i % 2 == 1 and q + 6 < 16:
-            r.append(k_read(*reads[q + 6]))
-        if i % 8 == 4 and dmas:
-            r += dmas.pop(0)
-        if kind == "full" and 26 <= i <= 30:
-            r.append(v_read(*V_SEQ[i - 26]))
-        if i == len(mf):
-            for d in dmas:
-                r += d
+            r += [k_read(*x, ks) for x in reads[pre:6]]
+        qq = i // 2
+        if i % 2 == 1 and qq + 6 < 16:
+            r.append(k_read(*reads[qq + 6], ks))
+        if i % 8 == 4:
+            r += dmas[i // 8]
+            if i // 8 == 3:
+                r += desc_advance("k")
+        if vre and i >= 26 and i % 2 == 0 and (i - 26) // 2 < len(vre):
+            r.append(v_read(*vre[(i - 26) // 2], q))
         return r
     o, left = schedule(mf, vl, side, carry=True)
     return out + o, left
 
 
-def block_b1(par, kind, masked, carried):
+def block_b1(q, kind, masked, carried):
     """P(j) V(j) for half 0 (16 MFMAs) while S(j+1) half 0 is exponentiated
     (first 16 of 32), P(j) half 1 packed and S(j+1) half 1's running max
     taken.  Returns (instructions, leftover VALU)."""
-    snxt = S_V[1 - par]
-    scur = S_V[par]
+    par = q % 2
+    snxt, scur = S_V[1 - par], S_V[par]
     pn = 1 - par
-    out = []
-    dmas = []
-    if kind != "last":
-        out += v_desc()
-        dmas = [dma("v", i) for i in range(4)]
     vl = list(carried)
     nc = len(vl)
     if kind != "last":
@@ -701,11 +706,12 @@ def block_b1(par, kind, masked, carried):
         if masked:
             vl += mask(snxt, 1)
         vl += running_max(snxt, 1, pn)
+    dmas = [dma("v", i, (q + 3) % 4) for i in range(4)] if kind != "last" else []
     if kind == "pre":
         o, _ = schedule([], vl)
         for d in dmas:
             o += d
-        return out + o, []
+        return o + desc_advance("v"), []
     mf = []
     for s2 in (0, 1):
         for db in range(4):
@@ -713,25 +719,25 @@ def block_b1(par, kind, masked, carried):
 
     def side(i):
         r = []
-        q = i // 2
-        if i % 2 == 1 and q + V_SETS - 1 < 16:
-            r.append(v_read(*V_SEQ[q + V_SETS - 1]))
+        qq = i // 2
+        if i % 2 == 1 and qq + V_SETS - 1 < 16:
+            r.append(v_read(*V_SEQ[qq + V_SETS - 1], q))
         if i % 4 == 2 and dmas:
-            r += dmas.pop(0)
-        if i == len(mf):
-            for d in dmas:
-                r += d
+            r += dmas[i // 4]
+            if i // 4 == 3:
+                r += desc_advance("v")
         return r
-    o, left = schedule(mf, vl, side, lead_cap=2, carry=True, n_carried=nc)
+    o, left = schedule(mf, vl, side, carry=True, n_carried=nc, lead_cap=0)
     for x in left:
         assert f"v{V_L}" not in x.wr, "the half-0 row sums must be added before the half-1 rescale"
-    return out + o, left
+    return o, left
 
 
-def block_b2(par, kind, carried):
+def block_b2(q, kind, carried):
     """P(j) V(j) for half 1 (16 MFMAs) while S(j+1) half 0's last 16
-    exponentials run and P(j) half 1 is summed; then the ring slots move on
-    and the next step's first K operands are read."""
+    exponentials run and P(j) half 1 is summed; then the next step's first
+    K(j+2) and V^T(j+1) operands are read."""
+    par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
     vl = list(carried)
     nc = len(vl)
@@ -739,8 +745,6 @@ def block_b2(par, kind, carried):
         vl += exps(snxt, 0, 16, 32)
     if kind != "pre":
         vl += sums(scur, 1)
-    if kind != "last":
-        vl += rotate_slots()
     mf = []
     if kind != "pre":
         for s2 in (2, 3):
@@ -749,12 +753,18 @@ def block_b2(par, kind, carried):
 
     def side(i):
         if i == len(mf):
-            return [k_read(0, kk) for kk in range(4)] if kind != "last" else []
-        q = 8 + i // 2
-        if i % 2 == 1 and q + V_SETS - 1 < 16:
-            return [v_read(*V_SEQ[q + V_SETS - 1])]
+            if kind == "last":
+                return []
+            # the pre step's own barrier: K(1) and V^T(0) have landed in
+            # every wave before they are read
+            sync = [waitcnt(vm=PRO_LATE), Ins("s_barrier", "barrier")] if kind == "pre" else []
+            return sync + ([k_read(0, kk, (q + 2) % 4) for kk in range(N_PRE_K)] +
+                           [v_read(*V_SEQ[k], (q + 1) % 4) for k in range(N_PRE_V)])
+        qq = 8 + i // 2
+        if i % 2 == 1 and qq + V_SETS - 1 < 16:
+            return [v_read(*V_SEQ[qq + V_SETS - 1], q)]
         return []
-    o, _ = schedule(mf, vl, side, lead_cap=2, n_carried=nc)
+    o, _ = schedule(mf, vl, side, n_carried=nc, lead_cap=2)
     return o
 
 
@@ -770,56 +780,21 @@ class Block:
         self.ret_point = ret_point    # the rescale routine may return here
 
 
-def rotate_slots():
-    """Step r -> r + 1: the K slot read and the K slot staged move one slot on
-    (four slots, offsets modulo 64 KiB); of the three V^T slots, the next
-    step reads the one V^T(r+1) went to (neither read nor staged in step r)
-    and stages into the one step r read.  The operand address registers move
-    with their slots; the M0 bases of the next step's DMAs follow."""
-    t0, t1 = sreg(S_T0), sreg(S_T1)
-    out = [
-        salu(f"s_add_u32 {sreg(S_RK)}, {sreg(S_RK)}, {TILE_BYTES}"),
-        salu(f"s_and_b32 {sreg(S_RK)}, {sreg(S_RK)}, {K_SLOTS * TILE_BYTES - 1}"),
-        salu(f"s_sub_u32 {t0}, {sreg(S_RK)}, {sreg(S_RK_OLD)}"),
-        salu(f"s_mov_b32 {sreg(S_RK_OLD)}, {sreg(S_RK)}"),
-        salu(f"s_add_u32 {sreg(S_WK)}, {sreg(S_WK)}, {TILE_BYTES}"),
-        salu(f"s_and_b32 {sreg(S_WK)}, {sreg(S_WK)}, {K_SLOTS * TILE_BYTES - 1}"),
-        salu(f"s_add_u32 {sreg(S_T2)}, {sreg(S_RV)}, {sreg(S_WV)}"),
-        salu(f"s_sub_u32 {sreg(S_T2)}, {V_SLOTS * TILE_BYTES}, {sreg(S_T2)}"),
-        salu(f"s_sub_u32 {t1}, {sreg(S_T2)}, {sreg(S_RV)}"),
-        salu(f"s_mov_b32 {sreg(S_WV)}, {sreg(S_RV)}"),
-        salu(f"s_mov_b32 {sreg(S_RV)}, {sreg(S_T2)}"),
-    ]
-    out += dma_bases()
-    for kk in range(8):
-        out.append(valu(f"v_add_u32 {vreg(KOFF_V + kk)}, {t0}, {vreg(KOFF_V + kk)}",
-                        {f"v{KOFF_V + kk}", f"s{S_T0}"}, {f"v{KOFF_V + kk}"}))
-    for s2 in range(4):
-        out.append(valu(f"v_add_u32 {vreg(VOFF_V + s2)}, {t1}, {vreg(VOFF_V + s2)}",
-                        {f"v{VOFF_V + s2}", f"s{S_T1}"}, {f"v{VOFF_V + s2}"}))
-    return out
-
-
-def dma_bases():
-    """M0 bases of a step's DMAs: K into S_WK, V^T into S_WV."""
-    return [salu(f"s_add_u32 {sreg(S_MK)}, {s_in('ldsw')}, {sreg(S_WK)}"),
-            salu(f"s_add_u32 {sreg(S_MV)}, {s_in('ldsw')}, {sreg(S_WV)}"),
-            salu(f"s_add_u32 {sreg(S_MV)}, {sreg(S_MV)}, {V_RING}")]
-
-
 def call_rescale(tag, par, h):
     """Blocks that apply O, l *= 2^-e(tile of parity par, half h) when that
-    tile half's flag is set: test, then (rarely) copy the exponents, drain
-    the LDS reads and branch to the shared routine with the return
-    address."""
+    tile half's flag is set: test, then (rarely) give each row block its
+    exponents, drain the LDS reads and branch to the shared routine with
+    the return address."""
     u = "%="
     flag = S_FLAG + 4 * par + 2 * h
     skip, pc = f"L{tag}_x_{u}", f"L{tag}_pc_{u}"
-    al = V_AL + 4 * par + 2 * h
+    al = V_AL + 2 * par + h
     test = Block(f"L{tag}_t_{u}", [salu(f"s_cmp_lg_u64 {sreg(flag, 2)}, 0"), branch("s_cbranch_scc0", skip)])
     call = Block(f"L{tag}_c_{u}", [
         valu(f"v_mov_b32 {vreg(V_RA)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA}"}),
-        valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al + 1)}", {f"v{al + 1}"}, {f"v{V_RA + 1}"}),
+        valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA + 1}"}),
+        Ins(f"v_permlane32_swap_b32 {vreg(V_RA)}, {vreg(V_RA + 1)}", "perm", {f"v{V_RA}", f"v{V_RA + 1}"},
+            {f"v{V_RA}", f"v{V_RA + 1}"}),
         waitcnt(lgkm=0),
         Ins(f"s_getpc_b64 {sreg(S_RET, 2)}", "salu", set(), {f"s{S_RET}", f"s{S_RET + 1}"}),
         label(pc),
@@ -830,42 +805,45 @@ def call_rescale(tag, par, h):
     return [test, call, Block(skip, [], ret_point=True)]
 
 
-def step_blocks(tag, par, kind, end_label):
+def step_blocks(tag, q, kind, end_label):
     """kind: 'pre' (S of the first tile only), 'full', 'last' (P V only).
-    A full step: wait and barrier, O, l *= alpha(j, 0) if needed, then an
-    unmasked or a masked copy of A, B1, O, l *= alpha(j, 1) if needed, B2."""
+    A full step: wait and barrier, O, l *= 2^-e(j, 0) if needed, then an
+    unmasked or a masked copy of A, B1, O, l *= 2^-e(j, 1) if needed, B2."""
     u = "%="
+    par = q % 2
     blocks = []
     if kind == "pre":
         # the first tile always takes the range mask (a no-op where all its
         # keys are legal)
-        a, left = block_a(par, "pre", True)
-        b1, left = block_b1(par, "pre", True, left)
-        b2 = block_b2(par, "pre", left)
-        blocks.append(Block(f"L{tag}_a_{u}", mask_test() + a + b1 + b2))
+        a, left = block_a(q, "pre", True)
+        b1, left = block_b1(q, "pre", True, left)
+        b2 = block_b2(q, "pre", left)
+        blocks.append(Block(f"L{tag}_a_{u}", a + b1 + b2))
         return blocks
     # DMAs issued two steps ago (and earlier) have landed in every wave; the
-    # 8 of the previous step may still be in flight, and so may the 4 K
-    # operand reads that step issued last (they read a slot no DMA of this
-    # step writes).
-    blocks.append(Block(f"L{tag}_s_{u}", [waitcnt(vm=8, lgkm=4), Ins("s_barrier", "barrier")]))
+    # 8 of the previous step may still be in flight, and so may the operand
+    # reads that step issued last (from slots no DMA of this step writes).
+    blocks.append(Block(f"L{tag}_s_{u}", [waitcnt(vm=8, lgkm=N_PRE_K + N_PRE_V), Ins("s_barrier", "barrier")]))
     blocks += call_rescale(f"{tag}r0", par, 0)
     if kind == "last":
-        a, left = block_a(par, "last", False)
-        b1, left = block_b1(par, "last", False, left)
+        a, left = block_a(q, "last", False)
+        b1, left = block_b1(q, "last", False, left)
         blocks.append(Block(f"L{tag}_a_{u}", a + b1))
         blocks += call_rescale(f"{tag}r1", par, 1)
-        blocks.append(Block(f"L{tag}_b2_{u}", block_b2(par, "last", left)))
+        blocks.append(Block(f"L{tag}_b2_{u}", block_b2(q, "last", left)))
         blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
         return blocks
-    blocks.append(Block(f"L{tag}_mt_{u}", mask_test() + [branch("s_cbranch_scc1", f"L{tag}_am_{u}")]))
+    # tile r + 1 needs the range mask iff it lies outside [it0, it1)
+    blocks.append(Block(f"L{tag}_mt_{u}", [salu(f"s_sub_u32 {sreg(S_T1)}, {sreg(S_R1)}, {s_in('it0')}"),
+                                           salu(f"s_cmp_ge_u32 {sreg(S_T1)}, {sreg(S_SPAN)}"),
+                                           branch("s_cbranch_scc1", f"L{tag}_am_{u}")]))
     for masked in (False, True):
         mt = "m" if masked else "u"
-        a, left = block_a(par, kind, masked)
-        b1, left = block_b1(par, kind, masked, left)
+        a, left = block_a(q, kind, masked)
+        b1, left = block_b1(q, kind, masked, left)
         blocks.append(Block(f"L{tag}_a{mt}_{u}", a + b1))
         blocks += call_rescale(f"{tag}{mt}r1", par, 1)
-        blocks.append(Block(f"L{tag}_b2{mt}_{u}", block_b2(par, kind, left)))
+        blocks.append(Block(f"L{tag}_b2{mt}_{u}", block_b2(q, kind, left)))
         if not masked:
             blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
     return blocks
@@ -873,7 +851,8 @@ def step_blocks(tag, par, kind, end_label):
 
 def prologue():
     """Q rows into their AGPRs, O = 0, constants, LDS operand addresses, the
-    first three K tiles and the first V^T tile staged, then wait and barrier."""
+    first three K tiles and the first two V^T tiles staged, then wait and
+    barrier."""
     # Every lane runs the loop; the compiler's code before this block wrote
     # some of the input SGPRs with VALU instructions (v_readfirstlane), and a
     # buffer instruction reading such an SGPR needs 5 wait states, which the
@@ -886,45 +865,39 @@ def prologue():
                            "vmem_ld", set(), regs("a", d, 4), vm=True))
     out += [
         salu(f"s_mov_b32 {sreg(S_N)}, {s_in('ntiles')}"),
-        salu(f"s_mov_b64 {sreg(S_KPTR, 2)}, {s_in('kbase')}"),
-        salu(f"s_mov_b32 {sreg(S_KRL)}, {s_in('krows')}"),
-        salu(f"s_mov_b64 {sreg(S_VPTR, 2)}, {s_in('vbase')}"),
+        salu(f"s_mov_b64 {sreg(S_KRS, 2)}, {s_in('kbase')}"),
+        salu(f"s_mov_b32 {sreg(S_KBYTES)}, {s_in('kbytes')}"),
+        salu(f"s_max_i32 {sreg(S_KRS + 2)}, {sreg(S_KBYTES)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_KRS + 3)}, {RSRC_WORD3:#x}"),
+        salu(f"s_mov_b64 {sreg(S_VRS, 2)}, {s_in('vbase')}"),
+        salu(f"s_lshl_b32 {sreg(S_VBYTES)}, {sreg(S_N)}, 14"),
+        salu(f"s_max_i32 {sreg(S_VRS + 2)}, {sreg(S_VBYTES)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_VRS + 3)}, {RSRC_WORD3:#x}"),
         salu(f"s_mov_b32 {sreg(S_EIGHT)}, {EIGHT_BITS:#x}"),
         salu(f"s_mov_b32 {sreg(S_SENT)}, {SENTINEL_BITS:#x}"),
+        salu(f"s_sub_i32 {sreg(S_SPAN)}, {s_in('it1')}, {s_in('it0')}"),
+        salu(f"s_max_i32 {sreg(S_SPAN)}, {sreg(S_SPAN)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_R1)}, 0"),
+        salu(f"s_mov_b32 {sreg(S_KEY0)}, {s_in('key0')}"),
     ]
     for f in range(4):
         out.append(salu(f"s_mov_b64 {sreg(S_FLAG + 2 * f, 2)}, 0"))
-    # K(0..2) -> K slots 0..2 (descriptors for tile r + 4 with r = -4..-2),
-    # V^T(0) -> V^T slot 0 (tile r + 2 with r = -2).
-    for r, slot in ((-4, 0), (-3, 1), (-2, 2)):
-        out.append(salu(f"s_mov_b32 {sreg(S_R)}, {r}"))
-        out += k_desc()
-        out.append(salu(f"s_add_u32 {sreg(S_MK)}, {s_in('ldsw')}, {slot * TILE_BYTES}"))
+    # K(0), K(1), V^T(0), K(2), V^T(1) into their slots, in the order the
+    # first steps need them: the pre step waits only for Q and K(0)
+    for kind, slot in (("k", 0), ("k", 1), ("v", 0), ("k", 2), ("v", 1)):
         for i in range(4):
-            out += dma("k", i)
-    out += v_desc()
-    out.append(salu(f"s_add_u32 {sreg(S_MV)}, {s_in('ldsw')}, {V_RING}"))
-    for i in range(4):
-        out += dma("v", i)
-    # State for step r = -1: K read slot 0, K staged into slot 3 (K(3)),
-    # V^T "read slot" 2 and V^T(1) staged into slot 1 (so that step 0 reads
-    # V^T slot 0 after the rotation).
-    out += [
-        salu(f"s_mov_b32 {sreg(S_R)}, -1"),
-        salu(f"s_mov_b32 {sreg(S_RK)}, 0"),
-        salu(f"s_mov_b32 {sreg(S_RK_OLD)}, 0"),
-        salu(f"s_mov_b32 {sreg(S_WK)}, {3 * TILE_BYTES}"),
-        salu(f"s_mov_b32 {sreg(S_RV)}, {2 * TILE_BYTES}"),
-        salu(f"s_mov_b32 {sreg(S_WV)}, {TILE_BYTES}"),
-    ]
-    out += dma_bases()
-    for i in range(128):
-        out.append(valu(f"v_accvgpr_write_b32 {areg(O_A + i)}, 0", set(), {f"a{O_A + i}"}))
+            out += dma(kind, i, slot)
+        out += desc_advance(kind)
+    # O = 0 by eight MFMAs of zero operands (instead of 128 AGPR writes)
+    z = PK_V
+    out += [valu(f"v_mov_b32 {vreg(z + k)}, 0", set(), {f"v{z + k}"}) for k in range(4)]
+    for blk in range(8):
+        out.append(mfma(("a", O_A + 16 * blk), ("v", z), ("v", z), False))
     for kk in range(8):
         out.append(valu(f"v_xor_b32 {vreg(KOFF_V + kk)}, {32 * kk}, {s_in('kofs')}", set(), {f"v{KOFF_V + kk}"}))
     for s2 in range(4):
         out.append(valu(f"v_xor_b32 {vreg(VOFF_V + s2)}, {32 * s2}, {s_in('vofs')}", set(), {f"v{VOFF_V + s2}"}))
-        out.append(valu(f"v_add_u32 {vreg(VOFF_V + s2)}, {V_RING + 2 * TILE_BYTES}, {vreg(VOFF_V + s2)}",
+        out.append(valu(f"v_add_u32 {vreg(VOFF_V + s2)}, {V_RING}, {vreg(VOFF_V + s2)}",
                         {f"v{VOFF_V + s2}"}, {f"v{VOFF_V + s2}"}))
     for rb in range(2):
         out += [
@@ -935,18 +908,19 @@ def prologue():
                  {f"v{V_SPAN + rb}"}),
             valu(f"v_mov_b32 {vreg(V_L + rb)}, 0", set(), {f"v{V_L + rb}"}),
         ]
-        for k in range(4):
-            out.append(valu(f"v_mov_b32 {vreg(V_AL + 2 * k + rb)}, 0", set(), {f"v{V_AL + 2 * k + rb}"}))
+    for k in range(4):
+        out.append(valu(f"v_mov_b32 {vreg(V_AL + k)}, 0", set(), {f"v{V_AL + k}"}))
     # n = -m c with m at the sentinel (no key seen yet)
     out += [valu(f"v_mov_b32 {vreg(V_NSENT)}, {sreg(S_SENT)}", {f"s{S_SENT}"}, {f"v{V_NSENT}"}),
             valu(f"v_mul_f32 {vreg(V_NSENT)}, {s_in('negc')}, {vreg(V_NSENT)}", {f"v{V_NSENT}"},
-                 {f"v{V_NSENT}"})]
-    for h in range(2):
-        for rb in range(2):
-            out.append(valu(f"v_mov_b32 {vreg(V_NMC + 2 * h + rb)}, {vreg(V_NSENT)}", {f"v{V_NSENT}"},
-                            {f"v{V_NMC + 2 * h + rb}"}))
+                 {f"v{V_NSENT}"}),
+            valu(f"v_mov_b32 {vreg(V_NMCC)}, {vreg(V_NSENT)}", {f"v{V_NSENT}"}, {f"v{V_NMCC}"})]
+    for k in range(4):
+        out.append(valu(f"v_mov_b32 {vreg(V_NMC + k)}, {vreg(V_NSENT)}", {f"v{V_NSENT}"}, {f"v{V_NMC + k}"}))
     out.append(valu(f"v_mov_b32 {vreg(V_NINF)}, {NEG_INF_BITS:#x}", set(), {f"v{V_NINF}"}))
-    out += [waitcnt(vm=0), Ins("s_barrier", "barrier")]
+    # Q and K(0) have landed in every wave (K(1), V^T(0), K(2), V^T(1) may
+    # still be in flight: 16 DMAs)
+    out += [waitcnt(vm=PRO_LATE), Ins("s_barrier", "barrier")]
     return out
 
 
@@ -1026,40 +1000,23 @@ def epilogue():
     return out
 
 
-def mask_test():
-    """S_KEY0 = first key of tile r + 1; SCC = that tile needs the range
-    mask (it lies outside [it0, it1))."""
-    t1 = sreg(S_T1)
-    return [salu(f"s_add_u32 {t1}, {sreg(S_R)}, 1"),
-            salu(f"s_lshl_b32 {sreg(S_KEY0)}, {t1}, 6"),
-            salu(f"s_add_u32 {sreg(S_KEY0)}, {sreg(S_KEY0)}, {s_in('key0')}"),
-            salu(f"s_cmp_lt_i32 {t1}, {s_in('it0')}"),
-            salu(f"s_cselect_b32 {sreg(S_MASK)}, 1, 0"),
-            salu(f"s_cmp_ge_i32 {t1}, {s_in('it1')}"),
-            salu(f"s_cselect_b32 {sreg(S_T0)}, 1, 0"),
-            salu(f"s_or_b32 {sreg(S_MASK)}, {sreg(S_MASK)}, {sreg(S_T0)}"),
-            salu(f"s_cmp_lg_u32 {sreg(S_MASK)}, 0")]
-
-
 def program():
     u = "%="
     blocks = [Block(f"Lpro_{u}", prologue() + [salu(f"s_cmp_le_i32 {sreg(S_N)}, 0"),
                                                   branch("s_cbranch_scc1", f"Lepi_{u}")])]
-    blocks += step_blocks("p", 1, "pre", None)
-    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R)}, 0")]))
-    t1 = sreg(S_T1)
-    for par in (0, 1):
-        blocks.append(Block(f"Lt{par}_{u}", [salu(f"s_add_u32 {t1}, {sreg(S_R)}, 1"),
-                                            salu(f"s_cmp_ge_i32 {t1}, {sreg(S_N)}"),
-                                            branch("s_cbranch_scc1", f"Llast{par}_{u}")]))
-        blocks += step_blocks(f"f{par}", par, "full", f"Linc{par}_{u}")
-        tail = [salu(f"s_add_u32 {sreg(S_R)}, {sreg(S_R)}, 1")]
-        if par == 1:
+    blocks += step_blocks("p", 3, "pre", None)
+    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R1)}, 1")]))
+    for q in range(4):
+        blocks.append(Block(f"Lt{q}_{u}", [salu(f"s_cmp_ge_i32 {sreg(S_R1)}, {sreg(S_N)}"),
+                                          branch("s_cbranch_scc1", f"Llast{q}_{u}")]))
+        blocks += step_blocks(f"f{q}", q, "full", f"Linc{q}_{u}")
+        tail = [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")]
+        if q == 3:
             tail.append(branch("s_branch", f"Lt0_{u}", cond=False))
-        blocks.append(Block(f"Linc{par}_{u}", tail))
-    for par in (0, 1):
-        bl = step_blocks(f"l{par}", par, "last", f"Lepi_{u}")
-        bl[0].name = f"Llast{par}_{u}"
+        blocks.append(Block(f"Linc{q}_{u}", tail))
+    for q in range(4):
+        bl = step_blocks(f"l{q}", q, "last", f"Lepi_{u}")
+        bl[0].name = f"Llast{q}_{u}"
         blocks += bl
     # the shared rescale routine (reached only by branches)
     blocks.append(Block(f"Lrescale_{u}", rescale_routine()))
@@ -1284,6 +1241,9 @@ def pad_program(blocks):
     return padded
 
 
+PAIR_AGE = 3         # MFMAs since a read was issued before it is taken as landed
+
+
 def insert_waits(blocks):
     """s_waitcnt lgkmcnt(n) before each use of an LDS read's result, with n
     the number of LDS operations issued after that read.  The queue of
@@ -1293,42 +1253,57 @@ def insert_waits(blocks):
     registers and are waited for explicitly at each step."""
     succ = successors(blocks)
     entry = [None] * len(blocks)
-    entry[0] = ([], set())
+    entry[0] = ([], ())
     out = []
     for i, b in enumerate(blocks):
         assert entry[i] is not None, f"block {b.name} has no forward predecessor"
         lg = [set(x) for x in entry[i][0]]
-        pend_vm = set(entry[i][1])          # registers of loads not yet waited for
+        born = [-PAIR_AGE] * len(lg)        # MFMA count when each read was issued
+        n_mf = 0
+        vmq = list(entry[i][1])             # outstanding memory operations (registers they load)
         res = []
         for ins in b.ins:
             if ins.kind == "wait":
                 mm = re.search(r"lgkmcnt\((\d+)\)", ins.text)
                 if mm:
                     k = int(mm.group(1))
-                    lg = lg[len(lg) - k:] if 0 < k < len(lg) else ([] if k == 0 else lg)
-                if "vmcnt(0)" in ins.text:
-                    pend_vm = set()
+                    if k < len(lg):
+                        lg, born = (lg[len(lg) - k:], born[len(born) - k:]) if k else ([], [])
+                mv = re.search(r"vmcnt\((\d+)\)", ins.text)
+                if mv:
+                    k = int(mv.group(1))
+                    vmq = vmq[len(vmq) - k:] if 0 < k < len(vmq) else ([] if k == 0 else vmq)
                 res.append(ins)
                 continue
             uses = ins.rd | ins.mask_rd | ins.wr
-            assert not (uses & pend_vm), f"memory load result used before vmcnt(0): {ins.text}"
+            pend_vm = set().union(*vmq) if vmq else set()
+            assert not (uses & pend_vm), f"memory load result used before its vmcnt wait: {ins.text}"
             w_l = None
             for k, regset in enumerate(lg):
                 if regset & uses:
                     w_l = len(lg) - k - 1
             if w_l is not None:
+                # an MFMA also waits for the next read when that one is old
+                # enough to have landed: the next MFMA then needs no wait
+                if ins.kind == "mfma" and w_l >= 1 and n_mf - born[len(lg) - w_l] >= PAIR_AGE:
+                    w_l -= 1
                 res.append(waitcnt(lgkm=w_l))
-                lg = lg[len(lg) - w_l:] if w_l > 0 else []
+                lg, born = (lg[len(lg) - w_l:], born[len(born) - w_l:]) if w_l > 0 else ([], [])
             if ins.lgkm and len(lg) >= 15:      # the lgkmcnt field holds at most 15
                 res.append(waitcnt(lgkm=7))
-                lg = lg[len(lg) - 7:]
+                lg, born = lg[len(lg) - 7:], born[len(born) - 7:]
             res.append(ins)
+            if ins.kind == "mfma":
+                n_mf += 1
             if ins.lgkm:
                 lg.append(set(ins.wr))
-            if ins.kind == "vmem_ld":
-                pend_vm |= ins.wr
+                born.append(n_mf)
+            if ins.vm:
+                vmq.append(frozenset(ins.wr) if ins.kind == "vmem_ld" else frozenset())
         out.append(res)
-        state = ([set(x) for x in lg], set(pend_vm))
+        # outstanding memory operations matter only while a load among them
+        # still has registers to wait for
+        state = ([set(x) for x in lg], tuple(vmq) if any(vmq) else ())
         for j in succ[i]:
             if entry[j] is None:
                 entry[j] = state
