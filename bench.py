@@ -158,7 +158,7 @@ def config_table(args):
 
 def p_sweep(args):
     """Config #3 (s16k) over router densities: the swattn_prefill_fwd call
-    (vt_pack_kernel + fwd_kernel) timed on its stream once the clock has
+    (vt_pack_kernel + the attention kernel) timed on its stream once the clock has
     settled, its routed TFLOP/s and fraction of the bf16 MFMA peak, and its
     time over the same call with every row routed full (dense causal) beside
     the routed-FLOP fraction."""
@@ -604,7 +604,8 @@ def main():
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
-                     "kernel": "swattn_prefill_fwd: vt_pack_kernel + fwd_kernel<false, false>",
+                     "kernel": ("swattn_prefill_fwd: vt_pack_kernel + fwd_wide_kernel<false> (the "
+                                "256-row kernel, which swattn_prefill_fwd picks at this grid size)"),
                      "kernel_ms": round(attn_ms, 4),
                      "kernel_timing": f"HIP events on the launch stream around "
                                       f"{attn_calls} back-to-back calls after {attn_warm} "
