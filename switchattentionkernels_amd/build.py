@@ -67,7 +67,7 @@ def compile_flags() -> list[str]:
     ]
 
 
-GENERATED = [("gen_fwd_wide.py", "swattn_fwd_wide.inc")]
+GENERATED = [("gen_fwd_wide.py", "swattn_fwd_wide.inc"), ("gen_bwd_dq.py", "swattn_bwd_dq.inc")]
 
 
 def generate_sources() -> None:

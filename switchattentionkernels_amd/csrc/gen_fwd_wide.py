@@ -492,7 +492,7 @@ def _dist(a, b):
     return 1
 
 
-def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
+def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2, one_feed=False):
     """Order one block: the MFMAs in their given order, side(i) (LDS reads,
     DMAs, descriptor updates) right before MFMA i and side(len) after the
     last, and the VALU / SALU list (in a valid program order) spread over
@@ -507,9 +507,11 @@ def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
     touch.  Dependent instructions keep the distance gfx950 needs between
     them.  Each gap takes at most one exponential, never as its first
     instruction; exponentials (and the FMAs that feed them), then urgent
-    work, go first among what is ready.  With carry, what does not fit is
-    returned for the next block instead of being issued after the last
-    MFMA."""
+    work, go first among what is ready.  With one_feed, a gap also takes at
+    most one instruction that feeds an exponential, so that the feeding
+    work keeps pace with the exponentials and can open the next gaps.  With
+    carry, what does not fit is returned for the next block instead of
+    being issued after the last MFMA."""
     n = len(valu_list)
     nm = len(mfmas)
     sides = [side(i) if side is not None else [] for i in range(nm + 1)]
@@ -540,7 +542,7 @@ def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
                 min_slot[j] = max(min_slot[j], i + 1)
         if any(_conflict(x, v) for x in sides[nm]):
             assert not carry, "a carried instruction conflicts with the block's last side work"
-    for j in range(n):
+    for j in reversed(range(n)):      # successors first: deadlines pass down whole chains
         for k in preds[j]:
             deadline[k] = min(deadline[k], deadline[j])
     issued = [False] * n
@@ -566,13 +568,15 @@ def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
             ready[k] = max(ready[k], st["pos"] - 1 + _dist(v, valu_list[k]))
         st["done"] += 1
 
-    def pick(slot, first, n_exp, relax=False):
+    def pick(slot, first, n_exp, n_feed=0, relax=False):
         best = None
         for j in range(n):
             if issued[j] or npred[j] or min_slot[j] > slot or (ready[j] > st["pos"] and not relax):
                 continue
             v = valu_list[j]
             if v.trans and (first or n_exp >= 1) and not relax:
+                continue
+            if one_feed and v.feeds_trans and n_feed >= 1 and not relax:
                 continue
             lead = v.trans or (v.feeds_trans and st["fed"] < 2)
             key = (not lead, not v.urgent, j)
@@ -581,16 +585,17 @@ def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2):
         return None if best is None else best[0]
 
     def fill(slot, cap, drain=False):
-        first, n_exp, cnt = True, 0, 0
+        first, n_exp, n_feed, cnt = True, 0, 0, 0
         while cnt < cap:
-            j = pick(slot, first, n_exp)
+            j = pick(slot, first, n_exp, n_feed)
             if j is None and drain:
-                j = pick(slot, first, n_exp, relax=True)
+                j = pick(slot, first, n_exp, n_feed, relax=True)
             if j is None:
                 break
             issue(j)
             first = False
             n_exp += valu_list[j].trans
+            n_feed += valu_list[j].feeds_trans
             cnt += 1
 
     def force(i):

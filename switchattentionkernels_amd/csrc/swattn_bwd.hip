@@ -55,9 +55,12 @@
 //   key-stationary pass, so every output is written once, deterministically.
 
 #include <limits.h>
-#include <algorithm>
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#include <algorithm>
 
+#include "swattn_bwd_dq.inc"
 #include "tiles.h"
 
 namespace swattn {
@@ -928,6 +931,206 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
   }
 }
 
+// ---------------------------------------------------------------------------
+// bwd_dq_wide_kernel: bwd_dq_kernel's work items with four waves of 64 rows,
+// one wave per SIMD.  Each K / V operand read from LDS then feeds two MFMAs
+// (both 32-row blocks of the wave), and the per-lane state (dQ^T, Q^T and
+// dO^T in AGPRs; two score tiles, the dP tile and the operand staging in
+// VGPRs) exceeds what a compiler-allocated kernel gets, so the tile loop is
+// the generated assembly of gen_bwd_dq.py.  This C++ part resolves the
+// rows, the tile range and pieces exactly as bwd_dq_kernel does and hands
+// the loop its per-lane inputs through LDS (the loop needs every VGPR).
+// ---------------------------------------------------------------------------
+constexpr int kDqWideLdsBytes = SWATTN_BWD_DQ_LDS_BYTES;
+static_assert(kDqWideLdsBytes == 8 * kTileBytes, "four-slot K and V rings of the generated loop");
+constexpr int kDqAuxGroups = SWATTN_BWD_DQ_AUX_GROUPS;
+// Per-lane inputs: group g of wave w at aux(w) + 1024 g + 16 lane, with
+// aux(w) in K slot 3 (waves 0-1) or V slot 3 (waves 2-3).
+__device__ __forceinline__ int dq_aux_offset(int wave) {
+  return wave < 2 ? 3 * kTileBytes + wave * kDqAuxGroups * 1024
+                  : 7 * kTileBytes + (wave - 2) * kDqAuxGroups * 1024;
+}
+static_assert(2 * kDqAuxGroups * 1024 <= kTileBytes, "two waves' inputs fit in a ring slot");
+
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void bwd_dq_wide_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kDqWideLdsBytes];
+  __shared__ int s_range[8];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, h = lane >> 5;
+  // Workgroup = ((row tile t, piece slot s), KV head) as in bwd_dq_kernel.
+  const int kvh = blockIdx.x % p.hkv;
+  const int ts = blockIdx.x / p.hkv;
+  const int full_slots = p.items[0] * p.dq_maxc[0];
+  const int t = ts < full_slots ? ts / p.dq_maxc[0]
+                                : p.items[0] + (ts - full_slots) / p.dq_maxc[1];
+  const int s_idx = ts < full_slots ? ts - t * p.dq_maxc[0]
+                                    : ts - full_slots - (t - p.items[0]) * p.dq_maxc[1];
+  const int b = t < p.items[0] ? 0 : 1;
+  const int item = b == 0 ? p.items[0] - 1 - t : p.items[0] + p.items[1] - 1 - t;
+
+  // This lane's two rows: row blocks 2 wave and 2 wave + 1 of the item.
+  float lse[2], delta[2];
+  int ks[2], ke[2], r[2];
+  int64_t row_off[2];
+  bool valid[2], has[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int blk = item * (kRowsPerItem / kBRows) + 2 * wave + rb;
+    const bool blk_ok = blk < p.blocks[b];
+    r[rb] = blk * kBRows + n;
+    valid[rb] = blk_ok && r[rb] < p.nrows[b];
+    lse[rb] = delta[rb] = 0.f;
+    ks[rb] = ke[rb] = 0;
+    row_off[rb] = -1;
+    if (valid[rb]) {
+      const float* inf = reinterpret_cast<const float*>(p.info + packed_block(p, b, kvh, blk) * kInfoBytes);
+      const int* infi = reinterpret_cast<const int*>(inf);
+      lse[rb] = inf[kInfoLse + n];
+      delta[rb] = inf[kInfoDelta + n];
+      ks[rb] = infi[kInfoStart + n];
+      ke[rb] = infi[kInfoEnd + n];
+      row_off[rb] = reinterpret_cast<const int64_t*>(inf)[kInfoRowOff + n];
+    }
+    has[rb] = valid[rb] && ks[rb] < ke[rb];
+  }
+  const int w_min_s = wave_min(min(has[0] ? ks[0] : INT_MAX, has[1] ? ks[1] : INT_MAX));
+  const int w_max_e = wave_max(max(has[0] ? ke[0] : INT_MIN, has[1] ? ke[1] : INT_MIN));
+  if (lane == 0) {
+    s_range[wave] = w_min_s;
+    s_range[4 + wave] = w_max_e;
+  }
+  __syncthreads();
+  int g_s = INT_MAX, g_e = INT_MIN;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    g_s = min(g_s, s_range[i]);
+    g_e = max(g_e, s_range[4 + i]);
+  }
+  const int t_all0 = g_e > g_s ? g_s / kBN : 0;
+  const int t_all1 = g_e > g_s ? (g_e + kBN - 1) / kBN : 0;
+  int t_begin = t_all0, t_end = t_all1;
+  bool piece = false;
+  if (p.dq_chunk > 0) {
+    const int len = t_all1 - t_all0;
+    const int nch = max(1, min(p.dq_maxc[b], (len + p.dq_chunk - 1) / p.dq_chunk));
+    if (s_idx >= nch) return;
+    if (s_idx == 0 && tid == 0) p.dq_nch[t * p.hkv + kvh] = nch;
+    piece = nch > 1;
+    const int plen = (len + nch - 1) / nch;
+    t_begin = t_all0 + min(len, s_idx * plen);
+    t_end = min(t_all1, t_begin + plen);
+  }
+  const int n_tiles = max(t_end - t_begin, 0);
+  // Tiles inside the range of every row this wave stores need no mask (a
+  // stored row with no key counts as start = +inf, end = -inf; lanes that
+  // store nothing do not count).
+  int ms = INT_MIN, me = INT_MAX;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    if (valid[rb]) {
+      ms = max(ms, has[rb] ? ks[rb] : INT_MAX);
+      me = min(me, has[rb] ? ke[rb] : INT_MIN);
+    }
+  }
+  const int w_max_s = __builtin_amdgcn_readfirstlane(wave_max(ms));
+  const int w_min_e = __builtin_amdgcn_readfirstlane(wave_min(me));
+  const int it0 = (w_max_s > INT_MAX - kBN ? INT_MAX / 2 : (w_max_s + kBN - 1) / kBN) - t_begin;
+  const int it1 = (w_min_e <= 0 ? 0 : w_min_e / kBN) - t_begin;
+
+  // Per-lane inputs of the loop, into LDS (read back by the same lane).
+  constexpr uint32_t kOff = 0x80000000u;   // beyond every descriptor's range: dropped
+  const uint32_t lds0 = lds_addr(smem);
+  uint32_t w[kDqAuxGroups * 4];
+  const int G = p.group;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    // dq row: every valid row is written (zeros for a row with no key)
+    const int q_slot = r[rb] / G;
+    const int pos = valid[rb] ? p.idx[b][q_slot] : 0;
+    const bool store = valid[rb] && pos_ok(p, pos);
+    const int qh = kvh * G + (r[rb] - q_slot * G);
+    w[0 + rb] = store ? static_cast<uint32_t>(((static_cast<int64_t>(pos) * p.hq + qh) * kD + 4 * h) * 2)
+                      : kOff;
+    w[2 + rb] = row_off[rb] >= 0 ? static_cast<uint32_t>(row_off[rb] * 2 + 16 * h) : kOff;
+    w[4 + rb] = __float_as_uint(-lse[rb]);
+    w[6 + rb] = __float_as_uint(delta[rb]);
+    w[8 + rb] = static_cast<uint32_t>(has[rb] ? ks[rb] - 4 * h : 0);
+    w[10 + rb] = static_cast<uint32_t>(has[rb] ? ke[rb] - ks[rb] : 0);
+  }
+  // Transposing reads of K^T (see read_xt): address of head_dim block db,
+  // read a, ring slot 0, k-step 0.
+  const int tj = (lane >> 2) & 3, tq = lane & 3, tdh = (lane >> 4) & 1;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int row = 8 * a + 4 * h + tj;
+    const int clo = 2 * tdh + (tq >> 1);
+    const uint32_t toff = lds0 + row * kRowBytes + ((clo ^ ((row >> 2) & 3)) << 4) + ((tq & 1) << 3);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) w[12 + 2 * db + a] = toff + (((db ^ tj) & 3) << 6);
+  }
+  // DMA offsets (16 key rows per wave, four rows per load) and the K row
+  // read address of k-step 0 (the loop XORs in 32 kk).
+  const uint32_t krowbytes = static_cast<uint32_t>(p.hkv) * kRowBytes;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * wave + 4 * i + (lane >> 4);
+    const int j = (lane & 15) ^ swz(row);
+    w[20 + i] = static_cast<uint32_t>(row) * krowbytes + 16 * j;
+  }
+  w[24] = lds0 + n * kRowBytes + ((h ^ swz(n)) << 4);
+  w[25] = w[26] = w[27] = 0;
+  {
+    uint4* aux = reinterpret_cast<uint4*>(smem + dq_aux_offset(wave) + 16 * lane);
+    // groups as the loop reads them: 0 dq / Q offsets, 1 -LSE / Delta, 2
+    // row bounds, 3-4 transposing read addresses, 5 DMA offsets, 6 K read
+    // address
+#pragma unroll
+    for (int g = 0; g < kDqAuxGroups; ++g)
+      aux[64 * g] = make_uint4(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+  }
+
+  const uint64_t kvoff = static_cast<uint64_t>(kvh) * kRowBytes +
+                         static_cast<uint64_t>(t_begin) * kBN * krowbytes;
+  const uint64_t kbase = reinterpret_cast<uint64_t>(p.k) + kvoff;
+  const uint64_t vbase = reinterpret_cast<uint64_t>(p.v) + kvoff;
+  // Bytes of K (and V) from the item's first tile to the end of its last
+  // tile or of the keys, whichever comes first (below 2^31: use_dq_wide).
+  const int64_t krows = min(static_cast<int64_t>(p.total_kv) - static_cast<int64_t>(t_begin) * kBN,
+                            static_cast<int64_t>(n_tiles) * kBN);
+  const int kbytes = static_cast<int>(max(krows, int64_t{0}) * krowbytes);
+  const uint32_t qbytes = static_cast<uint32_t>(p.total_q) * static_cast<uint32_t>(p.hq) * kRowBytes;
+  const i32x4 qrsrc = make_rsrc(p.q, qbytes);
+  const i32x4 dorsrc = make_rsrc(p.dout, qbytes);
+  const i32x4 dqrsrc = make_rsrc(p.dq, qbytes);
+  // This wave's pieces partials: units of row blocks 2 wave and 2 wave + 1.
+  const char* part = reinterpret_cast<const char*>(p.dq_part) +
+                     (static_cast<int64_t>(blockIdx.x) * kBwdWaves + 2 * wave) * kDqPartUnits * 1024;
+  const i32x4 prsrc = make_rsrc(piece ? part : reinterpret_cast<const char*>(p.dq), piece ? 2 * kDqPartUnits * 1024 : 0);
+  const uint32_t kb_lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(kbase));
+  const uint32_t kb_hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(kbase >> 32));
+  const uint32_t vb_lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(vbase));
+  const uint32_t vb_hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(vbase >> 32));
+  const uint64_t kb64 = (static_cast<uint64_t>(kb_hi) << 32) | kb_lo;
+  const uint64_t vb64 = (static_cast<uint64_t>(vb_hi) << 32) | vb_lo;
+  const float c = p.c, scale = p.scale;
+  asm volatile(SWATTN_BWD_DQ_ASM
+               :
+               : [kbase] "s"(kb64), [vbase] "s"(vb64), [qrsrc] "s"(qrsrc), [dorsrc] "s"(dorsrc),
+                 [dqrsrc] "s"(dqrsrc), [prsrc] "s"(prsrc),
+                 [ntiles] "s"(__builtin_amdgcn_readfirstlane(n_tiles)),
+                 [kbytes] "s"(__builtin_amdgcn_readfirstlane(kbytes)),
+                 [ktilebytes] "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(kBN * krowbytes))),
+                 [key0] "s"(__builtin_amdgcn_readfirstlane(t_begin * kBN)),
+                 [it0] "s"(__builtin_amdgcn_readfirstlane(it0)),
+                 [it1] "s"(__builtin_amdgcn_readfirstlane(it1)), [c] "s"(c), [scale] "s"(scale),
+                 [ldsw] "s"(__builtin_amdgcn_readfirstlane(lds0 + wave * 4096)),
+                 [aux] "s"(__builtin_amdgcn_readfirstlane(lds0 + dq_aux_offset(wave))),
+                 [piece] "s"(__builtin_amdgcn_readfirstlane(piece ? 1 : 0))
+               : SWATTN_BWD_DQ_CLOBBERS);
+}
+
 // dQ of row tiles cut into pieces: one thread per (row tile and KV head,
 // wave, float4 unit, lane); row tiles left whole were stored by the dQ
 // kernel.  It sums that unit over the pieces in piece order
@@ -984,6 +1187,18 @@ struct BwdLayout {
 };
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// bwd_dq_wide_kernel addresses Q, dO, dq and the item's K / V bytes with
+// 32-bit buffer offsets (and drops out-of-range ones): both must stay below
+// 2^31 bytes.  SWATTN_DQ_KERNEL=narrow / wide picks a kernel for tests and
+// comparisons.
+inline bool use_dq_wide(int64_t total_q, int64_t total_kv, int32_t heads_q, int32_t heads_kv) {
+  if (total_q * heads_q * kRowBytes >= (int64_t{1} << 31)) return false;
+  if (total_kv * heads_kv * kRowBytes >= (int64_t{1} << 31)) return false;
+  const char* force = getenv("SWATTN_DQ_KERNEL");
+  if (force != nullptr && strcmp(force, "narrow") == 0) return false;
+  return true;
+}
 
 inline BwdLayout bwd_layout(int64_t seq_kv, int64_t total_kv, int32_t heads_kv, int64_t group,
                             int32_t window, int64_t n_full, int64_t n_local) {
@@ -1197,8 +1412,11 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
   const int64_t q_items = (L.items[0] + L.items[1]) * heads_kv;
   if (q_items > 0) {
     const int64_t dq_wgs = (L.items[0] * L.dq_maxc[0] + L.items[1] * L.dq_maxc[1]) * heads_kv;
-    hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(dq_wgs)), dim3(kBwdThreads), 0,
-                       st, p);
+    if (use_dq_wide(total_q, total_kv, heads_q, heads_kv))
+      hipLaunchKernelGGL(bwd_dq_wide_kernel, dim3(static_cast<uint32_t>(dq_wgs)), dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL(bwd_dq_kernel, dim3(static_cast<uint32_t>(dq_wgs)), dim3(kBwdThreads), 0,
+                         st, p);
     if (L.dq_chunk > 0)
       hipLaunchKernelGGL(bwd_dq_reduce_kernel,
                          dim3(static_cast<uint32_t>(q_items * kBwdWaves * kDqPartUnits * 64 / kThreads)),
