@@ -67,7 +67,8 @@ def compile_flags() -> list[str]:
     ]
 
 
-GENERATED = [("gen_fwd_wide.py", "swattn_fwd_wide.inc"), ("gen_bwd_dq.py", "swattn_bwd_dq.inc")]
+GENERATED = [("gen_fwd_wide.py", "swattn_fwd_wide.inc"), ("gen_bwd_dq.py", "swattn_bwd_dq.inc"),
+             ("gen_bwd_dkdv.py", "swattn_bwd_dkdv.inc")]
 
 
 def generate_sources() -> None:

@@ -1,0 +1,620 @@
+"""Generates the block loop of ``bwd_dkdv_wide_kernel`` as gfx950 assembly.
+
+The arithmetic is the dK / dV part of the derivative of the reference branch
+kernel (swiattn_gqa_prefill_varlen.py V:176-241; the reference itself is
+forward-only, V:14-15): for each key j of a 256-key tile and each routed row
+r whose range holds it, P = 2^(c q_r.k_j - LSE_r) with the forward's log2
+LSE, dS = P (dO_r.v_j - Delta_r), both rounded to bf16 for the products,
+dv_j = sum_r P dO_r and dk_j = scale * sum_r dS q_r.  Keys outside a row's
+range get S = -inf, hence P = 0 and dS = 0.
+
+Layout.  A workgroup owns a (256-key tile, KV head) pair: four waves of 64
+keys (two 32-key halves "kh"), one wave per SIMD.  The dK^T and dV^T
+accumulators (128 d x 64 keys each, fp32) fill the 256 AGPRs; the wave's K
+rows (the B operands of S) sit in 64 VGPRs; the tile's V rows sit in LDS.
+The 32-row blocks of rows that can see the tile stream through a four-slot
+LDS ring (Q block, dO block), gathered from the rows' positions by 32-bit
+buffer offsets that bwd_prep_kernel writes into each block's 1 KiB info;
+the info blocks (LSE, Delta, key bounds, row offsets) travel through an
+eight-slot ring, each wave loading its own copy.  Four products per block,
+in the forms whose accumulators are the next products' B operands:
+
+  S    = Q K^T       (A: Q rows from LDS, B: K in VGPRs; lane = key)
+  dP   = dO V^T      (A: dO rows from LDS, B: V rows from LDS)
+  dV^T += dO^T P     (A: dO^T by transposing LDS reads, B: P packed)
+  dK^T += Q^T dS     (A: Q^T by transposing LDS reads, B: dS packed)
+
+Step r (phase q = r mod 4) issues S(r+1), dP(r+1) (32 MFMAs), then
+dV^T(r), dK^T(r) (32 MFMAs).  Its VALU work: the packing of dS(r) (before
+dP(r+1) overwrites it), P = 2^(S c - LSE) and dS = P (dP - Delta) of block
+r+1 in place (after the masking of block r+1 when some row of it does not
+see every key of the wave), and the packing of P(r+1) (after dV^T(r) has
+read P(r)).  It gathers block r+3's rows into ring slot (q+3) % 4 and loads
+block r+5's info.
+
+Register map (per lane; j = key in the half, hh = lane / 32):
+  a[0:127]    dK^T accumulators, (db, kh) at 32 db + 16 kh
+  a[128:255]  dV^T accumulators, likewise
+  v[0:63]     K operands, (kh, kk) at 32 kh + 4 kk
+  v[64:95]    S, kh at 64 + 16 kh (element e: row 8 (e >> 2) + 4 hh + (e & 3))
+  v[96:127]   dP, likewise (dS in place)
+  v[128:143]  P operands (bf16), (kh, s2) at 128 + 8 kh + 4 s2
+  v[144:159]  dS operands, likewise
+  v[160:191]  eight operand staging sets
+  v[192:255]  LDS addresses, LSE / Delta of four rows at a time, mask
+              temporaries, gather and store offsets
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+from gen_fwd_wide import (RSRC_WORD3, Block, Ins, areg, branch, insert_waits, mfma,  # noqa: E402
+                          pad_program, regs, s_in, salu, schedule, sreg, valu, vreg, waitcnt)
+
+# ---------------------------------------------------------------------------
+# registers
+# ---------------------------------------------------------------------------
+DK_A, DV_A = 0, 128
+KB_V = 0
+S_V, D_V = 64, 96
+PP_V, PD_V = 128, 144
+ST_V, N_SETS = 160, 8
+LEADM = 4                 # MFMAs between an operand's read and the first MFMA that takes it
+AOFF_V = 192              # [kk] Q / dO row read address (ring slot 0, Q part)
+VOFF_V = 200              # [kk] V row read address (key half 0)
+TOFF_V = 208              # [db][a] transposing read address (ring slot 0, Q part, k-step 0)
+V_LSE = 216               # [j' % 2][e]: LSE of row 8 j' + 4 hh + e
+V_DLT = 224               # Delta, likewise
+V_IRO = 232               # info read address: row offsets of this lane's gather rows
+V_ILH = 233               # info read address: this lane's rows (info slot of block r+1 + 16 hh)
+V_CH = 234                # [L] chunk offset of this lane's gather load L
+V_GT = 236                # [L] gather offsets; the mask flag's read
+V_KEY = 238               # this lane's key in half 0
+V_MK = 240                # 240..247 mask temporaries
+V_NINF = 248
+V_L16H = 249              # 16 hh
+V_LRO = 250               # 640 + 32 wave + 4 (lane >> 4): this lane's gather row offsets in an info block
+V_L16 = 251               # 16 lane
+V_TMP = 252
+V_DKOFF = 253             # [kh] dK / dV row byte offset (+ 8 hh)
+V_FA = 255                # the mask flag's read address
+
+S_T0, S_T1, S_T2, S_T3 = 52, 53, 54, 55
+S_R1 = 56                 # r + 1 for step r
+S_N = 57                  # block count
+S_MNEXT = 58              # block r + 1 needs the mask (set by step r - 1)
+S_KW1 = 59                # the wave's last key + 1
+S_PAIRS = (60, 62, 64, 66)
+S_INF = 68                # info slot base of block r + 1 (LDS address)
+S_SOFF = 69
+S_VRS = 72                # the V tile descriptor, advanced four rows per load
+S_VB = 76                 # V bytes from the descriptor base to the tile's end
+S_IS = 77                 # info slot of the info load
+S_FIRST, S_LASTC = 52, 77
+
+NEG_INF_BITS = 0xFF800000
+SLOT_BYTES = 16384        # Q block + dO block
+PART_DO = 8192
+RING = 65536              # ring base relative to the V tile
+INFO = RING + 4 * SLOT_BYTES
+INFO_SLOTS = 8
+LDS_BYTES = INFO + INFO_SLOTS * 1024
+AUX_GROUPS = 6
+AUX_OFF = RING + 2 * SLOT_BYTES   # ring slots 2-3 (the prologue gathers into 0-1)
+IW_LSE, IW_DLT, IW_ST, IW_EN = 0, 32, 64, 96   # info word offsets
+IW_MAXS, IW_MINE, IW_RO32 = 128, 129, 160
+
+# ---------------------------------------------------------------------------
+# operand loads and products
+# ---------------------------------------------------------------------------
+
+
+def st(o):
+    return ST_V + 4 * (o % N_SETS)
+
+
+def load_ins(ld, o, q):
+    """LDS reads of operand load ld (index o in the step) for phase q: the
+    step's S / dP block r+1 is in ring slot (q+1) % 4, its dV / dK block r
+    in slot q."""
+    kind = ld[0]
+    dst = st(o)
+    if kind in ("aq", "ad"):          # Q / dO rows of block r+1, k-step kk
+        kk = ld[1]
+        off = ((q + 1) % 4) * SLOT_BYTES + (PART_DO if kind == "ad" else 0)
+        return [Ins(f"ds_read_b128 {vreg(dst, 4)}, {vreg(AOFF_V + kk)} offset:{off}", "lds",
+                    {f"v{AOFF_V + kk}"}, regs("v", dst, 4), lgkm=True)]
+    if kind == "bv":                  # V rows of key half kh, k-step kk
+        kh, kk = ld[1], ld[2]
+        return [Ins(f"ds_read_b128 {vreg(dst, 4)}, {vreg(VOFF_V + kk)} offset:{kh * 8192}", "lds",
+                    {f"v{VOFF_V + kk}"}, regs("v", dst, 4), lgkm=True)]
+    # "tq" / "td": Q^T / dO^T of block r, k-step s2 (16 rows), d block db
+    s2, db = ld[1], ld[2]
+    off = q * SLOT_BYTES + (PART_DO if kind == "td" else 0) + 4096 * s2
+    out = []
+    for half in range(2):
+        adr = TOFF_V + 2 * db + half
+        out.append(Ins(f"ds_read_b64_tr_b16 {vreg(dst + 2 * half, 2)}, {vreg(adr)} offset:{off}", "lds",
+                       {f"v{adr}"}, regs("v", dst + 2 * half, 2), lgkm=True))
+    return out
+
+
+def step_ops(kind):
+    """(loads, mfmas): loads in issue order; each MFMA names the loads it
+    takes by index."""
+    loads, mf = [], []
+    if kind != "last":
+        for kk in range(8):                         # S(r+1)
+            loads.append(("aq", kk))
+            a = len(loads) - 1
+            for kh in range(2):
+                mf.append(("s", kh, kk, a, None))
+        for kk in range(8):                         # dP(r+1)
+            loads.append(("ad", kk))
+            a = len(loads) - 1
+            for kh in range(2):
+                loads.append(("bv", kh, kk))
+                mf.append(("d", kh, kk, a, len(loads) - 1))
+    if kind != "pre":
+        for part in ("td", "tq"):                   # dV^T(r), then dK^T(r)
+            for s2 in range(2):
+                for db in range(4):
+                    loads.append((part, s2, db))
+                    a = len(loads) - 1
+                    for kh in range(2):
+                        mf.append((part, kh, (s2, db), a, None))
+    return loads, mf
+
+
+def mfma_ins(m):
+    kind, kh, idx, a, b = m
+    if kind == "s":
+        kk = idx
+        return mfma(("v", S_V + 16 * kh), ("v", st(a)), ("v", KB_V + 32 * kh + 4 * kk), kk > 0)
+    if kind == "d":
+        kk = idx
+        return mfma(("v", D_V + 16 * kh), ("v", st(a)), ("v", st(b)), kk > 0)
+    s2, db = idx
+    if kind == "td":
+        return mfma(("a", DV_A + 32 * db + 16 * kh), ("v", st(a)), ("v", PP_V + 8 * kh + 4 * s2), True)
+    return mfma(("a", DK_A + 32 * db + 16 * kh), ("v", st(a)), ("v", PD_V + 8 * kh + 4 * s2), True)
+
+
+# ---------------------------------------------------------------------------
+# VALU work
+# ---------------------------------------------------------------------------
+
+
+def row_read(base, w0, jp):
+    """Four words (rows 8 j' + 4 hh .. +3) of block r+1's info field at word
+    w0, into base + 4 (j' % 2)."""
+    d = base + 4 * (jp % 2)
+    return Ins(f"ds_read_b128 {vreg(d, 4)}, {vreg(V_ILH)} offset:{4 * w0 + 32 * jp}", "lds", {f"v{V_ILH}"},
+               regs("v", d, 4), lgkm=True)
+
+
+def exps():
+    """P = 2^(S c - LSE) in place, rows four at a time (their LSE read just
+    before)."""
+    out = []
+    for jp in range(4):
+        out.append(row_read(V_LSE, IW_LSE, jp))
+        for e in range(4 * jp, 4 * jp + 4):
+            for kh in range(2):
+                x = S_V + 16 * kh + e
+                lse = V_LSE + 4 * (jp % 2) + (e & 3)
+                out.append(valu(f"v_fma_f32 {vreg(x)}, {vreg(x)}, {s_in('c')}, -{vreg(lse)}",
+                                {f"v{x}", f"v{lse}"}, {f"v{x}"}))
+                out[-1].feeds_trans = True
+                out.append(valu(f"v_exp_f32 {vreg(x)}, {vreg(x)}", {f"v{x}"}, {f"v{x}"}, trans=True))
+    return out
+
+
+def dss():
+    """dS = P (dP - Delta) in place in the dP registers."""
+    out = []
+    for jp in range(4):
+        out.append(row_read(V_DLT, IW_DLT, jp))
+        for e in range(4 * jp, 4 * jp + 4):
+            for kh in range(2):
+                x = S_V + 16 * kh + e
+                d = D_V + 16 * kh + e
+                dl = V_DLT + 4 * (jp % 2) + (e & 3)
+                out.append(valu(f"v_sub_f32 {vreg(d)}, {vreg(d)}, {vreg(dl)}", {f"v{d}", f"v{dl}"}, {f"v{d}"}))
+                out.append(valu(f"v_mul_f32 {vreg(d)}, {vreg(d)}, {vreg(x)}", {f"v{d}", f"v{x}"}, {f"v{d}"}))
+    return out
+
+
+def packs(src, dst):
+    """bf16 operands (kh, s2): register m of (kh, s2) holds elements 8 s2 +
+    2 m, +1 of half kh."""
+    out = []
+    for kh in range(2):
+        for s2 in range(2):
+            for m in range(4):
+                a = src + 16 * kh + 8 * s2 + 2 * m
+                d = dst + 8 * kh + 4 * s2 + m
+                out.append(valu(f"v_cvt_pk_bf16_f32 {vreg(d)}, {vreg(a)}, {vreg(a + 1)}",
+                                {f"v{a}", f"v{a + 1}"}, {f"v{d}"}))
+    return out
+
+
+def mask():
+    """S of block r+1 outside each row's [start, end) set to -inf: for each
+    group j' of four rows, key - start < end - start (unsigned) keeps it;
+    the key of half 1 is the key of half 0 plus 32."""
+    out = []
+    for jp in range(4):
+        out += _mask_group(jp)
+    return out
+
+
+def _mask_group(jp):
+    # starts into MK[0:4] (j' even) or MK[4:8] (j' odd); ends into the
+    # other four, each group's registers free again once its compares ran
+    st_r = V_MK + 4 * (jp % 2)
+    en_r = V_MK + 4 * (1 - jp % 2)
+    out = [Ins(f"ds_read_b128 {vreg(st_r, 4)}, {vreg(V_ILH)} offset:{4 * IW_ST + 32 * jp}", "lds",
+               {f"v{V_ILH}"}, regs("v", st_r, 4), lgkm=True),
+           Ins(f"ds_read_b128 {vreg(en_r, 4)}, {vreg(V_ILH)} offset:{4 * IW_EN + 32 * jp}", "lds",
+               {f"v{V_ILH}"}, regs("v", en_r, 4), lgkm=True)]
+    for e in range(4):
+        sr, er = st_r + e, en_r + e
+        out += [valu(f"v_sub_u32 {vreg(er)}, {vreg(er)}, {vreg(sr)}", {f"v{er}", f"v{sr}"}, {f"v{er}"}),
+                valu(f"v_sub_u32 {vreg(sr)}, {vreg(V_KEY)}, {vreg(sr)}", {f"v{V_KEY}", f"v{sr}"}, {f"v{sr}"})]
+        for kh in range(2):
+            p = S_PAIRS[kh]
+            x = S_V + 16 * kh + 4 * jp + e
+            if kh == 1:
+                out.append(valu(f"v_add_u32 {vreg(sr)}, 32, {vreg(sr)}", {f"v{sr}"}, {f"v{sr}"}))
+            out += [valu(f"v_cmp_gt_u32_e64 {sreg(p, 2)}, {vreg(er)}, {vreg(sr)}", {f"v{er}", f"v{sr}"},
+                         {f"s{p}", f"s{p + 1}"}),
+                    valu(f"v_cndmask_b32_e64 {vreg(x)}, {vreg(V_NINF)}, {vreg(x)}, {sreg(p, 2)}",
+                         {f"v{x}", f"v{V_NINF}"}, {f"v{x}"}, mask_rd={f"s{p}", f"s{p + 1}"})]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# block bookkeeping: packed block of list index a, info loads, row gathers,
+# the mask flag
+# ---------------------------------------------------------------------------
+
+
+def block_index(sdst, rel):
+    """sdst = packed block of list index a = min(r + rel, n - 1) (S_R1 = r
+    + 1): a + pb0 for a < n0, else a + pb1 (pb1 already less n0)."""
+    return [salu(f"s_add_u32 {sreg(sdst)}, {sreg(S_R1)}, {rel - 1}"),
+            salu(f"s_add_u32 {sreg(S_T3)}, {sreg(S_N)}, -1"),
+            salu(f"s_min_i32 {sreg(sdst)}, {sreg(sdst)}, {sreg(S_T3)}"),
+            salu(f"s_cmp_lt_i32 {sreg(sdst)}, {s_in('n0')}"),
+            salu(f"s_cselect_b32 {sreg(S_T3)}, {s_in('pb0')}, {s_in('pb1')}"),
+            salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {sreg(S_T3)}")]
+
+
+def info_slot(sdst, rel):
+    """sdst = LDS address of the info slot of list index r + rel."""
+    return [salu(f"s_add_u32 {sreg(sdst)}, {sreg(S_R1)}, {rel - 1}"),
+            salu(f"s_and_b32 {sreg(sdst)}, {sreg(sdst)}, {INFO_SLOTS - 1}"),
+            salu(f"s_lshl_b32 {sreg(sdst)}, {sreg(sdst)}, 10"),
+            salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {s_in('info0')}")]
+
+
+def info_dma(rel, split=False):
+    """Block r+rel's 1 KiB info into its info slot (every wave its own
+    copy, so that each wave waits only for its own load).  The whole offset
+    is in the lane's offset register, where the descriptor's range check
+    sees it.  With split, (address work, the load) as two groups: the load's
+    M0 write may then be issued ahead of its slot's other work."""
+    prep = block_index(S_T0, rel) + info_slot(S_IS, rel)
+    prep += [salu(f"s_lshl_b32 {sreg(S_T0)}, {sreg(S_T0)}, 10"),
+             valu(f"v_add_u32 {vreg(V_TMP)}, {sreg(S_T0)}, {vreg(V_L16)}", {f"s{S_T0}", f"v{V_L16}"},
+                  {f"v{V_TMP}"})]
+    issue = [salu(f"s_mov_b32 m0, {sreg(S_IS)}", wr={"m0"}),
+             Ins(f"buffer_load_dwordx4 {vreg(V_TMP)}, {s_in('irsrc')}, 0 offen lds", "dma",
+                 {"m0", f"v{V_TMP}"}, set(), vm=True)]
+    return (prep, issue) if split else prep + issue
+
+
+def gather(rel, slot):
+    """This wave's share of block r+rel's rows into ring slot `slot`: loads
+    L = 2 w, 2 w + 1 of the Q part and of the dO part (rows 4 L .. 4 L + 3),
+    each lane fetching its chunk at its row's offset."""
+    out = info_slot(S_T1, rel)
+    out += [valu(f"v_add_u32 {vreg(V_IRO)}, {sreg(S_T1)}, {vreg(V_LRO)}", {f"s{S_T1}", f"v{V_LRO}"},
+                 {f"v{V_IRO}"})]
+    for L in range(2):
+        out.append(Ins(f"ds_read_b32 {vreg(V_GT + L)}, {vreg(V_IRO)} offset:{16 * L}", "lds", {f"v{V_IRO}"},
+                       {f"v{V_GT + L}"}, lgkm=True))
+    for L in range(2):
+        out.append(valu(f"v_add_u32 {vreg(V_GT + L)}, {vreg(V_GT + L)}, {vreg(V_CH + L)}",
+                        {f"v{V_GT + L}", f"v{V_CH + L}"}, {f"v{V_GT + L}"}))
+    for part, rs in ((0, "qrsrc"), (PART_DO, "dorsrc")):
+        for L in range(2):
+            base = RING + slot * SLOT_BYTES + part
+            out += [salu(f"s_add_u32 m0, {s_in('wl')}, {base + 1024 * L}", wr={"m0"}),
+                    Ins(f"buffer_load_dwordx4 {vreg(V_GT + L)}, {s_in(rs)}, 0 offen lds", "dma",
+                        {f"v{V_GT + L}", "m0"}, set(), vm=True)]
+    return out
+
+
+def mask_flag(rel):
+    """S_MNEXT = block r+rel has a row whose range does not hold every key of
+    the wave (from its bounds summary)."""
+    out = info_slot(S_T1, rel)
+    out += [valu(f"v_mov_b32 {vreg(V_FA)}, {sreg(S_T1)}", {f"s{S_T1}"}, {f"v{V_FA}"}),
+            Ins(f"ds_read_b64 {vreg(V_GT, 2)}, {vreg(V_FA)} offset:{4 * IW_MAXS}", "lds", {f"v{V_FA}"},
+                regs("v", V_GT, 2), lgkm=True),
+            valu(f"v_readfirstlane_b32 {sreg(S_T2)}, {vreg(V_GT)}", {f"v{V_GT}"}, {f"s{S_T2}"}),
+            valu(f"v_readfirstlane_b32 {sreg(S_T3)}, {vreg(V_GT + 1)}", {f"v{V_GT + 1}"}, {f"s{S_T3}"}),
+            Ins("s_nop 4", "nop"),
+            salu(f"s_cmp_gt_i32 {sreg(S_T2)}, {s_in('kw0')}", {f"s{S_T2}"}),
+            salu(f"s_cselect_b32 {sreg(S_MNEXT)}, 1, 0", wr={f"s{S_MNEXT}"}),
+            salu(f"s_cmp_lt_i32 {sreg(S_T3)}, {sreg(S_KW1)}", {f"s{S_T3}", f"s{S_KW1}"}),
+            salu(f"s_cselect_b32 {sreg(S_T2)}, 1, 0", wr={f"s{S_T2}"}),
+            salu(f"s_or_b32 {sreg(S_MNEXT)}, {sreg(S_MNEXT)}, {sreg(S_T2)}", {f"s{S_MNEXT}", f"s{S_T2}"},
+                 {f"s{S_MNEXT}"})]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# steps
+# ---------------------------------------------------------------------------
+# Step r (phase q): S(r+1), dP(r+1) from block r+1's rows in ring slot
+# (q+1) % 4, dV^T(r), dK^T(r) from block r's rows in slot q.  It gathers
+# block r+3 into slot (q+3) % 4 (block r-1's, last read by step r-1), loads
+# block r+5's info and reads block r+2's bounds summary for the next step's
+# mask choice.
+
+
+def _spread(items, nm, lo=0.1, hi=0.75):
+    """Side positions for a list of instruction groups, spread over the
+    MFMA slots between fractions lo and hi of the step."""
+    n = len(items)
+    out = {}
+    for k, it in enumerate(items):
+        pos = int(nm * (lo + (hi - lo) * k / max(1, n - 1)))
+        out.setdefault(max(1, min(nm - 1, pos)), []).extend(it)
+    return out
+
+
+def step_code(q, kind, masked):
+    loads, mfs = step_ops(kind)
+    mf = [mfma_ins(m) for m in mfs]
+    nm = len(mf)
+    first_use, last_use = {}, {}
+    for i, m in enumerate(mfs):
+        for a in (m[3], m[4]):
+            if a is not None:
+                first_use.setdefault(a, i)
+                last_use[a] = i
+    # operand o is read LEADM MFMAs before its first use, but only once the
+    # previous load of its staging set has been taken by its last MFMA
+    reads = {}
+    for o, ld in enumerate(loads):
+        at = first_use[o] - LEADM
+        if o >= N_SETS:
+            at = max(at, last_use[o - N_SETS] + 1)
+        at = max(at, 0)
+        reads.setdefault(at, []).extend(load_ins(ld, o, q))
+    side_extra = {}
+    if kind != "last":
+        g = gather(3, (q + 3) % 4)
+        ip, ii = info_dma(5, split=True)
+        groups = [mask_flag(2), g[:9]] + [g[9 + 2 * k: 11 + 2 * k] for k in range(4)] + [ip, ii]
+        side_extra = _spread(groups, nm)
+
+    def side(i):
+        return side_extra.get(i, []) + reads.get(i, [])
+
+    carried = []
+    if kind != "pre":
+        carried = packs(D_V, PD_V)           # dS(r), before dP(r+1) overwrites it
+    vl = list(carried)
+    if kind != "last":
+        if masked:
+            vl += mask()
+        vl += exps() + dss() + packs(S_V, PP_V)
+    o, _ = schedule(mf, vl, side, carry=False, n_carried=len(carried), lead_cap=4, one_feed=True)
+    return o
+
+
+def step_blocks(tag, q, kind, end_label):
+    u = "%="
+    if kind == "pre":
+        return [Block(f"L{tag}_a_{u}", step_code(q, "pre", True))]
+    # block r+1's rows (gathered two steps ago) have landed in every wave;
+    # the previous step's five loads may still be in flight
+    blocks = [Block(f"L{tag}_s_{u}", [waitcnt(vm=5, lgkm=0), Ins("s_barrier", "barrier")])]
+    if kind == "last":
+        blocks.append(Block(f"L{tag}_a_{u}", step_code(q, "last", False)
+                            + [branch("s_branch", end_label, cond=False)]))
+        return blocks
+    blocks.append(Block(f"L{tag}_mt_{u}", [salu(f"s_cmp_lg_u32 {sreg(S_MNEXT)}, 0"),
+                                           branch("s_cbranch_scc1", f"L{tag}_am_{u}")]))
+    blocks.append(Block(f"L{tag}_au_{u}", step_code(q, "full", False)
+                        + [branch("s_branch", end_label, cond=False)]))
+    blocks.append(Block(f"L{tag}_am_{u}", step_code(q, "full", True)))
+    return blocks
+
+
+def prologue():
+    """Per-lane inputs from LDS, K rows into their VGPRs, the V tile into
+    LDS, dK^T = dV^T = 0, the info of blocks 0..3; once blocks 0-1's info
+    has landed their rows, block 0's info read base and block 1's mask
+    flag; wait and barrier."""
+    out = [salu("s_mov_b64 exec, -1"), Ins("s_nop 7", "nop")]
+    t = V_TMP
+    out += [valu(f"v_mbcnt_lo_u32_b32 {vreg(t)}, -1, 0", set(), {f"v{t}"}),
+            valu(f"v_mbcnt_hi_u32_b32 {vreg(t)}, -1, {vreg(t)}", {f"v{t}"}, {f"v{t}"}),
+            valu(f"v_lshlrev_b32 {vreg(V_L16)}, 4, {vreg(t)}", {f"v{t}"}, {f"v{V_L16}"}),
+            valu(f"v_add_u32 {vreg(t)}, {s_in('aux')}, {vreg(V_L16)}", {f"v{V_L16}"}, {f"v{t}"})]
+    # input groups (four words per lane): 0 K load offsets (kh), dK / dV row
+    # offsets (kh); 1 A and V read address bases, gather chunk offsets (L);
+    # 2-3 transposing read addresses; 4 V tile DMA offsets (i mod 4); 5 the
+    # key of half 0, 16 hh, this lane's gather row-offset position, unused
+    dst = {0: S_V, 1: S_V + 4, 2: TOFF_V, 3: TOFF_V + 4, 4: S_V + 8, 5: S_V + 12}
+    for g in range(AUX_GROUPS):
+        d = dst[g]
+        out.append(Ins(f"ds_read_b128 {vreg(d, 4)}, {vreg(t)} offset:{g * 1024}", "lds", {f"v{t}"},
+                       regs("v", d, 4), lgkm=True))
+    out += [salu(f"s_mov_b32 {sreg(S_N)}, {s_in('nblk')}"),
+            salu(f"s_add_u32 {sreg(S_KW1)}, {s_in('kw0')}, 64"),
+            salu(f"s_mov_b32 {sreg(S_R1)}, 0"),
+            salu(f"s_mov_b64 {sreg(S_VRS, 2)}, {s_in('vbase')}"),
+            salu(f"s_mov_b32 {sreg(S_VB)}, {s_in('vbytes')}"),
+            salu(f"s_max_i32 {sreg(S_VRS + 2)}, {sreg(S_VB)}, 0"),
+            salu(f"s_mov_b32 {sreg(S_VRS + 3)}, {RSRC_WORD3:#x}")]
+    # K rows: (kh, kk) at 32 kh + 4 kk
+    for kh in range(2):
+        for kk in range(8):
+            d = KB_V + 32 * kh + 4 * kk
+            out.append(Ins(f"buffer_load_dwordx4 {vreg(d, 4)}, {vreg(S_V + kh)}, {s_in('krsrc')}, 0 offen "
+                           f"offset:{32 * kk}", "vmem_ld", {f"v{S_V + kh}"}, regs("v", d, 4), vm=True))
+    # the V tile: this wave's 64 rows, four per load, the descriptor moved
+    # on four rows per load (the rows past the keys' end fall outside it)
+    for i in range(16):
+        if i:
+            out += [salu(f"s_add_u32 {sreg(S_VRS)}, {sreg(S_VRS)}, {s_in('krow4')}"),
+                    salu(f"s_addc_u32 {sreg(S_VRS + 1)}, {sreg(S_VRS + 1)}, 0"),
+                    salu(f"s_sub_i32 {sreg(S_VB)}, {sreg(S_VB)}, {s_in('krow4')}"),
+                    salu(f"s_max_i32 {sreg(S_VRS + 2)}, {sreg(S_VB)}, 0")]
+        out += [salu(f"s_add_u32 m0, {s_in('vl')}, {1024 * i}", wr={"m0"}),
+                Ins(f"buffer_load_dwordx4 {vreg(S_V + 8 + (i % 4))}, {sreg(S_VRS, 4)}, 0 offen lds",
+                    "dma", {f"v{S_V + 8 + (i % 4)}", "m0"} | regs("s", S_VRS, 4), set(), vm=True)]
+    # per-lane state from the inputs
+    out += [valu(f"v_mov_b32 {vreg(V_DKOFF + kh)}, {vreg(S_V + 2 + kh)}", {f"v{S_V + 2 + kh}"},
+                 {f"v{V_DKOFF + kh}"}) for kh in range(2)]
+    out += [valu(f"v_mov_b32 {vreg(V_CH + L)}, {vreg(S_V + 6 + L)}", {f"v{S_V + 6 + L}"}, {f"v{V_CH + L}"})
+            for L in range(2)]
+    out += [valu(f"v_mov_b32 {vreg(V_KEY)}, {vreg(S_V + 12)}", {f"v{S_V + 12}"}, {f"v{V_KEY}"}),
+            valu(f"v_mov_b32 {vreg(V_L16H)}, {vreg(S_V + 13)}", {f"v{S_V + 13}"}, {f"v{V_L16H}"}),
+            valu(f"v_mov_b32 {vreg(V_LRO)}, {vreg(S_V + 14)}", {f"v{S_V + 14}"}, {f"v{V_LRO}"})]
+    for kk in range(8):
+        out.append(valu(f"v_xor_b32 {vreg(AOFF_V + kk)}, {32 * kk}, {vreg(S_V + 4)}", {f"v{S_V + 4}"},
+                        {f"v{AOFF_V + kk}"}))
+        out.append(valu(f"v_xor_b32 {vreg(VOFF_V + kk)}, {32 * kk}, {vreg(S_V + 5)}", {f"v{S_V + 5}"},
+                        {f"v{VOFF_V + kk}"}))
+    out.append(valu(f"v_mov_b32 {vreg(V_NINF)}, {NEG_INF_BITS:#x}", set(), {f"v{V_NINF}"}))
+    # dK^T = dV^T = 0 by sixteen MFMAs of zero operands
+    z = V_MK
+    out += [valu(f"v_mov_b32 {vreg(z + k)}, 0", set(), {f"v{z + k}"}) for k in range(4)]
+    for blk in range(16):
+        out.append(mfma(("a", 16 * blk), ("v", z), ("v", z), False))
+    # info of blocks 0..3 (S_R1 = 0 here: list index r + rel with r = -1)
+    for b in range(4):
+        out += info_dma(b + 1)
+    # blocks 0-1's info has landed (this wave's own loads; 2-3 may still be
+    # in flight), and every wave has read its inputs
+    out += [waitcnt(vm=2, lgkm=0), Ins("s_barrier", "barrier")]
+    out += gather(1, 0) + gather(2, 1)
+    out += step_prefix(1)
+    out += mask_flag(2)
+    # block 0's rows have landed in every wave (block 1's four loads may
+    # still be in flight)
+    out += [waitcnt(vm=4), Ins("s_barrier", "barrier")]
+    return out
+
+
+def step_prefix(rel=1):
+    """The info read base (+ 16 hh) of block r+rel, r+1 = S_R1."""
+    return info_slot(S_INF, rel) + [valu(f"v_add_u32 {vreg(V_ILH)}, {sreg(S_INF)}, {vreg(V_L16H)}",
+                                         {f"s{S_INF}", f"v{V_L16H}"}, {f"v{V_ILH}"})]
+
+
+def epilogue():
+    """dK = scale dK^T and dV = dV^T as bf16 rows, four values per store, at
+    each lane's key row (keys past the end fall outside the descriptors)."""
+    out = [waitcnt(vm=0, lgkm=0)]
+    for acc, rs, scl in ((DK_A, "dkrsrc", True), (DV_A, "dvrsrc", False)):
+        for kh in range(2):
+            for db in range(4):
+                tv = 64 + 16 * ((2 * kh + db) % 4)
+                for k in range(16):
+                    a = acc + 32 * db + 16 * kh + k
+                    out.append(valu(f"v_accvgpr_read_b32 {vreg(tv + k)}, {areg(a)}", {f"a{a}"}, {f"v{tv + k}"}))
+                if scl:
+                    for k in range(16):
+                        out.append(valu(f"v_mul_f32 {vreg(tv + k)}, {s_in('scale')}, {vreg(tv + k)}",
+                                        {f"v{tv + k}"}, {f"v{tv + k}"}))
+                for jj in range(4):
+                    for k in range(2):
+                        out.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 4 * jj + k)}, {vreg(tv + 4 * jj + 2 * k)}, "
+                                        f"{vreg(tv + 4 * jj + 2 * k + 1)}",
+                                        {f"v{tv + 4 * jj + 2 * k}", f"v{tv + 4 * jj + 2 * k + 1}"},
+                                        {f"v{tv + 4 * jj + k}"}))
+                    out.append(Ins(f"buffer_store_dwordx2 {vreg(tv + 4 * jj, 2)}, {vreg(V_DKOFF + kh)}, "
+                                   f"{s_in(rs)}, 0 offen offset:{64 * db + 16 * jj}", "vmem_st",
+                                   regs("v", tv + 4 * jj, 2) | {f"v{V_DKOFF + kh}"}, set(), vm=True))
+    return out
+
+
+def program():
+    u = "%="
+    blocks = [Block(f"Lpro_{u}", prologue() + [salu(f"s_cmp_le_i32 {sreg(S_N)}, 0"),
+                                                  branch("s_cbranch_scc1", f"Lepi_{u}")])]
+    blocks += step_blocks("p", 3, "pre", None)
+    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R1)}, 1")] + step_prefix(1)))
+    for q in range(4):
+        blocks.append(Block(f"Lt{q}_{u}", [salu(f"s_cmp_ge_i32 {sreg(S_R1)}, {sreg(S_N)}"),
+                                          branch("s_cbranch_scc1", f"Llast{q}_{u}")]))
+        blocks += step_blocks(f"f{q}", q, "full", f"Linc{q}_{u}")
+        tail = [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")] + step_prefix(1)
+        if q == 3:
+            tail.append(branch("s_branch", f"Lt0_{u}", cond=False))
+        blocks.append(Block(f"Linc{q}_{u}", tail))
+    for q in range(4):
+        bl = step_blocks(f"l{q}", q, "last", f"Lepi_{u}")
+        bl[0].name = f"Llast{q}_{u}"
+        blocks += bl
+    blocks.append(Block(f"Lepi_{u}", epilogue()))
+    return blocks
+
+
+def generate():
+    blocks = program()
+    waited = insert_waits(blocks)
+    for b, w in zip(blocks, waited):
+        b.ins = w
+    padded = pad_program(blocks)
+    lines = []
+    for b, ins_list in zip(blocks, padded):
+        lines.append(f"{b.name}:")
+        for ins in ins_list:
+            lines.append("  " + ins.text)
+    return lines
+
+
+def clobbers():
+    c = [f"v{i}" for i in range(256)] + [f"a{i}" for i in range(256)]
+    c += [f"s{i}" for i in range(S_FIRST, S_LASTC + 1)]
+    c += ["vcc", "exec", "m0", "memory"]
+    return c
+
+
+def emit(path):
+    lines = generate()
+    with open(path, "w") as f:
+        f.write("// Generated by gen_bwd_dkdv.py: the block loop of bwd_dkdv_wide_kernel.  Do not edit.\n")
+        f.write("#pragma once\n")
+        f.write("#define SWATTN_BWD_DKDV_ASM \\\n")
+        for ln in lines:
+            f.write(f'  "{ln}\\n" \\\n')
+        f.write('  ""\n')
+        f.write(f"#define SWATTN_BWD_DKDV_LDS_BYTES {LDS_BYTES}\n")
+        f.write(f"#define SWATTN_BWD_DKDV_AUX_GROUPS {AUX_GROUPS}\n")
+        f.write(f"#define SWATTN_BWD_DKDV_AUX_OFF {AUX_OFF}\n")
+        f.write(f"#define SWATTN_BWD_DKDV_INFO_OFF {INFO}\n")
+        f.write(f"#define SWATTN_BWD_DKDV_RING_OFF {RING}\n")
+        f.write("#define SWATTN_BWD_DKDV_CLOBBERS \\\n  ")
+        f.write(", ".join(f'"{x}"' for x in clobbers()))
+        f.write("\n")
+    return len(lines)
+
+
+if __name__ == "__main__":
+    n = emit(sys.argv[1])
+    print(f"{n} lines")

@@ -60,6 +60,7 @@
 #include <string.h>
 #include <algorithm>
 
+#include "swattn_bwd_dkdv.inc"
 #include "swattn_bwd_dq.inc"
 #include "tiles.h"
 
@@ -77,6 +78,7 @@ constexpr int kInfoBytes = 1024;                       // row info block
 constexpr int kInfoLse = 0, kInfoDelta = 32, kInfoStart = 64, kInfoEnd = 96;   // word offsets
 constexpr int kInfoMaxStart = 128, kInfoMinEnd = 129;
 constexpr int kInfoRowOff = 96;                        // int64 offset: row element offsets (bytes 768..1023)
+constexpr int kInfoRowOff32 = 160;                     // word offset: row byte offsets (bytes 640..767)
 constexpr int kKeysDkv = kBwdWaves * 32;               // keys per dK/dV workgroup (32 per wave)
 constexpr int kRowsPerItem = kBwdWaves * 32;           // rows per dQ workgroup (32 per wave)
 constexpr int kVTileBytes = kKeysDkv * kRowBytes;      // the dK/dV workgroup's V rows: 64 KiB
@@ -241,6 +243,11 @@ __global__ __launch_bounds__(kThreads) void bwd_prep_kernel(const BwdParams p) {
     infi[kInfoStart + rr] = live ? ks : 0;
     infi[kInfoEnd + rr] = live ? ke : 0;
     reinterpret_cast<int64_t*>(inf)[kInfoRowOff + rr] = live ? row_off : -1;
+    // The same as a 32-bit byte offset for bwd_dkdv_wide_kernel's buffer
+    // loads (only used where Q is below 2^31 bytes; past every range when
+    // the row contributes nothing, so that its loads read zeros).
+    reinterpret_cast<uint32_t*>(inf)[kInfoRowOff32 + rr] =
+        live ? static_cast<uint32_t>(row_off * 2) : 0x80000000u;
     s_ks[rr] = live ? ks : INT_MAX;   // a dead row forces the mask on its block
     s_ke[rr] = live ? ke : INT_MIN;
   }
@@ -633,6 +640,118 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_dkdv_wide_kernel: bwd_dkdv_kernel's (key tile, KV head) pairs with four
+// waves of 64 keys, one wave per SIMD, for grids that need no split.  Each
+// LDS read of a block's Q or dO operand then feeds two MFMAs (both 32-key
+// halves of the wave), and the per-lane state (dK^T and dV^T in AGPRs; K,
+// the score and dP tiles and their bf16 packs in VGPRs) exceeds what a
+// compiler-allocated kernel gets, so the block loop is the generated
+// assembly of gen_bwd_dkdv.py.  This C++ part resolves the pair, its row
+// blocks and the per-lane offsets, and hands them to the loop through LDS.
+// ---------------------------------------------------------------------------
+constexpr int kDkvWideLdsBytes = SWATTN_BWD_DKDV_LDS_BYTES;
+constexpr int kDkvAuxGroups = SWATTN_BWD_DKDV_AUX_GROUPS;
+static_assert(SWATTN_BWD_DKDV_RING_OFF == kVTileBytes, "the V tile precedes the row ring");
+static_assert(4 * kDkvAuxGroups * 1024 <= 2 * 2 * kBlockBytes, "the inputs fit in ring slots 2-3");
+
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void bwd_dkdv_wide_kernel(const BwdParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kDkvWideLdsBytes];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, hh = lane >> 5;
+  int t, kvh;
+  dkv_pair(p, blockIdx.x, t, kvh);
+  const int nt = p.kv_tiles_dkv;
+  const int b0lo = p.ranges[2 * t], b0hi = p.ranges[2 * t + 1];
+  const int b1lo = p.ranges[2 * (nt + t)], b1hi = p.ranges[2 * (nt + t) + 1];
+  const int n0 = max(b0hi - b0lo, 0), n1 = max(b1hi - b1lo, 0);
+  const int nb = n0 + n1;
+  const int pb0 = static_cast<int>(packed_block(p, 0, kvh, b0lo));
+  const int pb1 = static_cast<int>(packed_block(p, 1, kvh, b1lo)) - n0;
+  const int kw0 = t * kKeysDkv + 64 * wave;
+  const uint32_t krowbytes = static_cast<uint32_t>(p.hkv) * kRowBytes;
+  const uint32_t lds0 = lds_addr(smem);
+  constexpr uint32_t kOff = 0x80000000u;   // beyond every descriptor's range: dropped
+
+  // Per-lane inputs of the loop (group g at aux + 1024 g + 16 lane).
+  uint32_t w[kDkvAuxGroups * 4];
+#pragma unroll
+  for (int kh = 0; kh < 2; ++kh) {
+    const int key = kw0 + 32 * kh + j;
+    const bool in = key < p.total_kv;
+    const uint32_t row = static_cast<uint32_t>(key) * static_cast<uint32_t>(p.hkv) + kvh;
+    w[kh] = in ? row * kRowBytes + 16 * hh : kOff;
+    w[2 + kh] = in ? row * kRowBytes + 8 * hh : kOff;
+  }
+  w[4] = lds0 + kVTileBytes + j * kRowBytes + ((hh ^ swz(j)) << 4);
+  w[5] = lds0 + (64 * wave + j) * kRowBytes + ((hh ^ swz(j)) << 4);
+#pragma unroll
+  for (int L = 0; L < 2; ++L)
+    w[6 + L] = 16 * ((lane & 15) ^ ((((lane >> 4) & 3) << 2) | ((2 * wave + L) & 3)));
+  const int tj = (lane >> 2) & 3, tq = lane & 3, tdh = (lane >> 4) & 1;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int row = 8 * a + 4 * hh + tj;
+    const int clo = 2 * tdh + (tq >> 1);
+    const uint32_t toff = lds0 + kVTileBytes + row * kRowBytes + ((clo ^ ((row >> 2) & 3)) << 4) + ((tq & 1) << 3);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) w[8 + 2 * db + a] = toff + (((db ^ tj) & 3) << 6);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    w[16 + q] = (64 * wave + (lane >> 4)) * krowbytes +
+                16 * ((lane & 15) ^ ((((lane >> 4) & 3) << 2) | q));
+  w[20] = kw0 + j;
+  w[21] = 16 * hh;
+  w[22] = 4 * kInfoRowOff32 + 32 * wave + 4 * (lane >> 4);
+  w[23] = 0;
+  const uint32_t aux = lds0 + SWATTN_BWD_DKDV_AUX_OFF + wave * kDkvAuxGroups * 1024;
+  {
+    uint4* a = reinterpret_cast<uint4*>(smem + (aux - lds0) + 16 * lane);
+#pragma unroll
+    for (int g = 0; g < kDkvAuxGroups; ++g)
+      a[64 * g] = make_uint4(w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]);
+  }
+
+  const uint32_t qbytes = static_cast<uint32_t>(p.total_q) * static_cast<uint32_t>(p.hq) * kRowBytes;
+  const uint32_t kvbytes = static_cast<uint32_t>(p.total_kv) * krowbytes;
+  const i32x4 qrsrc = make_rsrc(p.q, qbytes);
+  const i32x4 dorsrc = make_rsrc(p.dout, qbytes);
+  const uint32_t nblocks = static_cast<uint32_t>(p.blk_base[1] + static_cast<int64_t>(p.hkv) * p.blocks[1]);
+  const i32x4 irsrc = make_rsrc(p.info, nblocks * kInfoBytes);
+  const i32x4 krsrc = make_rsrc(p.k, kvbytes);
+  const i32x4 dkrsrc = make_rsrc(p.dk, kvbytes);
+  const i32x4 dvrsrc = make_rsrc(p.dv, kvbytes);
+  // The V tile: from its first key row (head kvh) to the end of V.
+  const uint64_t vbase = reinterpret_cast<uint64_t>(p.v) +
+                         (static_cast<uint64_t>(t) * kKeysDkv * p.hkv + kvh) * kRowBytes;
+  const int vbytes = static_cast<int>(static_cast<int64_t>(kvbytes) -
+                                      static_cast<int64_t>(t) * kKeysDkv * krowbytes -
+                                      static_cast<int64_t>(kvh) * kRowBytes);
+  const uint32_t vb_lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(vbase));
+  const uint32_t vb_hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(vbase >> 32));
+  const uint64_t vb64 = (static_cast<uint64_t>(vb_hi) << 32) | vb_lo;
+  const float c = p.c, scale = p.scale;
+  asm volatile(SWATTN_BWD_DKDV_ASM
+               :
+               : [qrsrc] "s"(qrsrc), [dorsrc] "s"(dorsrc), [irsrc] "s"(irsrc), [krsrc] "s"(krsrc),
+                 [dkrsrc] "s"(dkrsrc), [dvrsrc] "s"(dvrsrc), [vbase] "s"(vb64),
+                 [vbytes] "s"(__builtin_amdgcn_readfirstlane(vbytes)),
+                 [nblk] "s"(__builtin_amdgcn_readfirstlane(nb)),
+                 [n0] "s"(__builtin_amdgcn_readfirstlane(n0)),
+                 [pb0] "s"(__builtin_amdgcn_readfirstlane(pb0)),
+                 [pb1] "s"(__builtin_amdgcn_readfirstlane(pb1)),
+                 [kw0] "s"(__builtin_amdgcn_readfirstlane(kw0)),
+                 [krow4] "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(4 * krowbytes))),
+                 [vl] "s"(__builtin_amdgcn_readfirstlane(lds0 + 64 * wave * kRowBytes)),
+                 [wl] "s"(__builtin_amdgcn_readfirstlane(lds0 + 2048 * wave)),
+                 [info0] "s"(__builtin_amdgcn_readfirstlane(lds0 + SWATTN_BWD_DKDV_INFO_OFF)),
+                 [aux] "s"(__builtin_amdgcn_readfirstlane(aux)), [c] "s"(c), [scale] "s"(scale)
+               : SWATTN_BWD_DKDV_CLOBBERS);
 }
 
 // dK / dV of split pairs: one thread per (pair, wave, float4 unit, lane).
@@ -1192,6 +1311,22 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // 32-bit buffer offsets (and drops out-of-range ones): both must stay below
 // 2^31 bytes.  SWATTN_DQ_KERNEL=narrow / wide picks a kernel for tests and
 // comparisons.
+// bwd_dkdv_wide_kernel gathers rows by 32-bit offsets into Q / dO and reads
+// K, V, dK, dV and the row info through 32-bit buffer ranges (all below
+// 2^31 bytes).  It runs where the pairs need no split;
+// SWATTN_DKDV_KERNEL=narrow picks the eight-wave kernel everywhere, =wide
+// the 64-key kernel also where the eight-wave one would split (tests).
+inline bool use_dkdv_wide(int64_t total_q, int64_t total_kv, int32_t heads_q, int32_t heads_kv,
+                          int64_t total_blocks, int64_t split) {
+  if (total_q * heads_q * kRowBytes >= (int64_t{1} << 31)) return false;
+  if (total_kv * heads_kv * kRowBytes >= (int64_t{1} << 31)) return false;
+  if (total_blocks * kInfoBytes >= (int64_t{1} << 31)) return false;
+  const char* force = getenv("SWATTN_DKDV_KERNEL");
+  if (force != nullptr && strcmp(force, "narrow") == 0) return false;
+  if (force != nullptr && strcmp(force, "wide") == 0) return true;
+  return split == 1;
+}
+
 inline bool use_dq_wide(int64_t total_q, int64_t total_kv, int32_t heads_q, int32_t heads_kv) {
   if (total_q * heads_q * kRowBytes >= (int64_t{1} << 31)) return false;
   if (total_kv * heads_kv * kRowBytes >= (int64_t{1} << 31)) return false;
@@ -1403,9 +1538,16 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
                          dim3(kThreads), 0, st, p);
   }
   const int64_t pairs = L.kv_tiles_dkv * heads_kv;
-  hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(pairs * L.dkv_split)),
-                     dim3(kBwdThreads), 0, st, p);
-  if (L.dkv_split > 1)
+  const bool dkdv_wide = use_dkdv_wide(total_q, total_kv, heads_q, heads_kv, L.total_blocks, L.dkv_split);
+  if (dkdv_wide) {
+    BwdParams pw = p;
+    pw.dkv_split = 1;   // every pair whole: no partials
+    hipLaunchKernelGGL(bwd_dkdv_wide_kernel, dim3(static_cast<uint32_t>(pairs)), dim3(256), 0, st, pw);
+  } else {
+    hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(pairs * L.dkv_split)),
+                       dim3(kBwdThreads), 0, st, p);
+  }
+  if (!dkdv_wide && L.dkv_split > 1)
     hipLaunchKernelGGL(bwd_dkdv_reduce_kernel,
                        dim3(static_cast<uint32_t>(pairs * kBwdWaves * kPartUnits * 64 / kThreads)),
                        dim3(kThreads), 0, st, p);
