@@ -28,13 +28,15 @@ its own S buffer, and the transposing reads deliver the keys of each
 lanes.
 
 Step r (phase q = r mod 4, tile r's S in buffer r mod 2) issues 96 MFMAs:
-dQ^T(r) for keys 0-31, S^T(r+1) keys 0-31, dP^T(r+1) keys 0-31, S^T(r+1)
-keys 32-63, dQ^T(r) keys 32-63, dP^T(r+1) keys 32-63.  Its VALU work: dS of
-tile r's keys 32-63 and their packing (before the dQ^T MFMAs that read
-them), P = 2^(S c - LSE) of tile r+1 (after the masking of tile r+1 when
-it lies outside the range every row of the wave covers), dS of tile r+1's
-keys 0-31 and their packing.  A list scheduler spreads it over the MFMA
-slots.  K and V tiles stream through four-slot LDS rings, staged by the
+dQ^T(r) for keys 0-15, S^T(r+1) (keys 0-31, then 32-63), dQ^T(r) keys
+16-31, dP^T(r+1) keys 0-31, dQ^T(r) keys 32-63, dP^T(r+1) keys 32-63, so
+that the scores of tile r+1 are complete early and their exponentials can
+spread over the rest of the step.  Its VALU work: dS of tile r's keys 32-63
+and their packing (before the dQ^T MFMAs that read them), P = 2^(S c -
+LSE) of tile r+1 (after the masking of tile r+1 when it lies outside the
+range every row of the wave covers), dS of tile r+1's keys 0-31 and their
+packing.  A list scheduler spreads it over the MFMA slots, at most one
+exponential and one instruction feeding an exponential per slot.  K and V tiles stream through four-slot LDS rings, staged by the
 four waves with global -> LDS loads three (K) and four (V) steps ahead;
 the loop is unrolled four steps so that every LDS address is a base
 register plus an immediate offset.
