@@ -15,8 +15,9 @@ rows (the B operands of S) sit in 64 VGPRs; the tile's V rows sit in LDS.
 The 32-row blocks of rows that can see the tile stream through a four-slot
 LDS ring (Q block, dO block), gathered from the rows' positions by 32-bit
 buffer offsets that bwd_prep_kernel writes into each block's 1 KiB info;
-the info blocks (LSE, Delta, key bounds, row offsets) travel through an
-eight-slot ring, each wave loading its own copy.  Four products per block,
+the info blocks (LSE, Delta, key bounds, row offsets) travel through a
+four-slot ring, each wave loading its own copy, so that every info read is
+a fixed register plus an immediate offset.  Four products per block,
 in the forms whose accumulators are the next products' B operands:
 
   S    = Q K^T       (A: Q rows from LDS, B: K in VGPRs; lane = key)
@@ -29,8 +30,8 @@ dV^T(r), dK^T(r) (32 MFMAs).  Its VALU work: the packing of dS(r) (before
 dP(r+1) overwrites it), P = 2^(S c - LSE) and dS = P (dP - Delta) of block
 r+1 in place (after the masking of block r+1 when some row of it does not
 see every key of the wave), and the packing of P(r+1) (after dV^T(r) has
-read P(r)).  It gathers block r+3's rows into ring slot (q+3) % 4 and loads
-block r+5's info.
+read P(r)).  It loads block r+4's info into info slot q and gathers block
+r+3's rows into ring slot (q+3) % 4.
 
 Register map (per lane; j = key in the half, hh = lane / 32):
   a[0:127]    dK^T accumulators, (db, kh) at 32 db + 16 kh
@@ -69,19 +70,17 @@ VOFF_V = 200              # [kk] V row read address (key half 0)
 TOFF_V = 208              # [db][a] transposing read address (ring slot 0, Q part, k-step 0)
 V_LSE = 216               # [j' % 2][e]: LSE of row 8 j' + 4 hh + e
 V_DLT = 224               # Delta, likewise
-V_IRO = 232               # info read address: row offsets of this lane's gather rows
-V_ILH = 233               # info read address: this lane's rows (info slot of block r+1 + 16 hh)
+V_IRO = 232               # info ring + this lane's gather row offsets (slot 0)
+V_ILH = 233               # info ring + 16 hh: this lane's rows (slot 0)
 V_CH = 234                # [L] chunk offset of this lane's gather load L
 V_GT = 236                # [L] gather offsets; the mask flag's read
 V_KEY = 238               # this lane's key in half 0
 V_MK = 240                # 240..247 mask temporaries
 V_NINF = 248
-V_L16H = 249              # 16 hh
-V_LRO = 250               # 640 + 32 wave + 4 (lane >> 4): this lane's gather row offsets in an info block
 V_L16 = 251               # 16 lane
 V_TMP = 252
 V_DKOFF = 253             # [kh] dK / dV row byte offset (+ 8 hh)
-V_FA = 255                # the mask flag's read address
+V_FA = 255                # the info ring (slot 0): the bounds summary reads
 
 S_T0, S_T1, S_T2, S_T3 = 52, 53, 54, 55
 S_R1 = 56                 # r + 1 for step r
@@ -89,7 +88,6 @@ S_N = 57                  # block count
 S_MNEXT = 58              # block r + 1 needs the mask (set by step r - 1)
 S_KW1 = 59                # the wave's last key + 1
 S_PAIRS = (60, 62, 64, 66)
-S_INF = 68                # info slot base of block r + 1 (LDS address)
 S_SOFF = 69
 S_VRS = 72                # the V tile descriptor, advanced four rows per load
 S_VB = 76                 # V bytes from the descriptor base to the tile's end
@@ -101,7 +99,7 @@ SLOT_BYTES = 16384        # Q block + dO block
 PART_DO = 8192
 RING = 65536              # ring base relative to the V tile
 INFO = RING + 4 * SLOT_BYTES
-INFO_SLOTS = 8
+INFO_SLOTS = 4
 LDS_BYTES = INFO + INFO_SLOTS * 1024
 AUX_GROUPS = 6
 AUX_OFF = RING + 2 * SLOT_BYTES   # ring slots 2-3 (the prologue gathers into 0-1)
@@ -189,20 +187,20 @@ def mfma_ins(m):
 # ---------------------------------------------------------------------------
 
 
-def row_read(base, w0, jp):
-    """Four words (rows 8 j' + 4 hh .. +3) of block r+1's info field at word
-    w0, into base + 4 (j' % 2)."""
+def row_read(base, w0, jp, slot):
+    """Four words (rows 8 j' + 4 hh .. +3) of the info field at word w0 of
+    info slot `slot`, into base + 4 (j' % 2)."""
     d = base + 4 * (jp % 2)
-    return Ins(f"ds_read_b128 {vreg(d, 4)}, {vreg(V_ILH)} offset:{4 * w0 + 32 * jp}", "lds", {f"v{V_ILH}"},
-               regs("v", d, 4), lgkm=True)
+    return Ins(f"ds_read_b128 {vreg(d, 4)}, {vreg(V_ILH)} offset:{1024 * slot + 4 * w0 + 32 * jp}", "lds",
+               {f"v{V_ILH}"}, regs("v", d, 4), lgkm=True)
 
 
-def exps():
+def exps(slot):
     """P = 2^(S c - LSE) in place, rows four at a time (their LSE read just
-    before)."""
+    before from info slot `slot`)."""
     out = []
     for jp in range(4):
-        out.append(row_read(V_LSE, IW_LSE, jp))
+        out.append(row_read(V_LSE, IW_LSE, jp, slot))
         for e in range(4 * jp, 4 * jp + 4):
             for kh in range(2):
                 x = S_V + 16 * kh + e
@@ -214,11 +212,11 @@ def exps():
     return out
 
 
-def dss():
+def dss(slot):
     """dS = P (dP - Delta) in place in the dP registers."""
     out = []
     for jp in range(4):
-        out.append(row_read(V_DLT, IW_DLT, jp))
+        out.append(row_read(V_DLT, IW_DLT, jp, slot))
         for e in range(4 * jp, 4 * jp + 4):
             for kh in range(2):
                 x = S_V + 16 * kh + e
@@ -243,24 +241,25 @@ def packs(src, dst):
     return out
 
 
-def mask():
+def mask(slot):
     """S of block r+1 outside each row's [start, end) set to -inf: for each
     group j' of four rows, key - start < end - start (unsigned) keeps it;
     the key of half 1 is the key of half 0 plus 32."""
     out = []
     for jp in range(4):
-        out += _mask_group(jp)
+        out += _mask_group(jp, slot)
     return out
 
 
-def _mask_group(jp):
+def _mask_group(jp, slot):
     # starts into MK[0:4] (j' even) or MK[4:8] (j' odd); ends into the
     # other four, each group's registers free again once its compares ran
     st_r = V_MK + 4 * (jp % 2)
     en_r = V_MK + 4 * (1 - jp % 2)
-    out = [Ins(f"ds_read_b128 {vreg(st_r, 4)}, {vreg(V_ILH)} offset:{4 * IW_ST + 32 * jp}", "lds",
+    base = 1024 * slot
+    out = [Ins(f"ds_read_b128 {vreg(st_r, 4)}, {vreg(V_ILH)} offset:{base + 4 * IW_ST + 32 * jp}", "lds",
                {f"v{V_ILH}"}, regs("v", st_r, 4), lgkm=True),
-           Ins(f"ds_read_b128 {vreg(en_r, 4)}, {vreg(V_ILH)} offset:{4 * IW_EN + 32 * jp}", "lds",
+           Ins(f"ds_read_b128 {vreg(en_r, 4)}, {vreg(V_ILH)} offset:{base + 4 * IW_EN + 32 * jp}", "lds",
                {f"v{V_ILH}"}, regs("v", en_r, 4), lgkm=True)]
     for e in range(4):
         sr, er = st_r + e, en_r + e
@@ -295,40 +294,30 @@ def block_index(sdst, rel):
             salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {sreg(S_T3)}")]
 
 
-def info_slot(sdst, rel):
-    """sdst = LDS address of the info slot of list index r + rel."""
-    return [salu(f"s_add_u32 {sreg(sdst)}, {sreg(S_R1)}, {rel - 1}"),
-            salu(f"s_and_b32 {sreg(sdst)}, {sreg(sdst)}, {INFO_SLOTS - 1}"),
-            salu(f"s_lshl_b32 {sreg(sdst)}, {sreg(sdst)}, 10"),
-            salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {s_in('info0')}")]
-
-
-def info_dma(rel, split=False):
-    """Block r+rel's 1 KiB info into its info slot (every wave its own
+def info_dma(rel, slot):
+    """Block r+rel's 1 KiB info into info slot `slot` (every wave its own
     copy, so that each wave waits only for its own load).  The whole offset
     is in the lane's offset register, where the descriptor's range check
-    sees it.  With split, (address work, the load) as two groups: the load's
-    M0 write may then be issued ahead of its slot's other work."""
-    prep = block_index(S_T0, rel) + info_slot(S_IS, rel)
-    prep += [salu(f"s_lshl_b32 {sreg(S_T0)}, {sreg(S_T0)}, 10"),
-             valu(f"v_add_u32 {vreg(V_TMP)}, {sreg(S_T0)}, {vreg(V_L16)}", {f"s{S_T0}", f"v{V_L16}"},
-                  {f"v{V_TMP}"})]
-    issue = [salu(f"s_mov_b32 m0, {sreg(S_IS)}", wr={"m0"}),
-             Ins(f"buffer_load_dwordx4 {vreg(V_TMP)}, {s_in('irsrc')}, 0 offen lds", "dma",
-                 {"m0", f"v{V_TMP}"}, set(), vm=True)]
-    return (prep, issue) if split else prep + issue
+    sees it."""
+    out = block_index(S_T0, rel)
+    out += [salu(f"s_lshl_b32 {sreg(S_T0)}, {sreg(S_T0)}, 10"),
+            valu(f"v_add_u32 {vreg(V_TMP)}, {sreg(S_T0)}, {vreg(V_L16)}", {f"s{S_T0}", f"v{V_L16}"},
+                 {f"v{V_TMP}"}),
+            salu(f"s_add_u32 m0, {s_in('info0')}, {1024 * slot}", wr={"m0"}),
+            Ins(f"buffer_load_dwordx4 {vreg(V_TMP)}, {s_in('irsrc')}, 0 offen lds", "dma",
+                {"m0", f"v{V_TMP}"}, set(), vm=True)]
+    return out
 
 
-def gather(rel, slot):
-    """This wave's share of block r+rel's rows into ring slot `slot`: loads
-    L = 2 w, 2 w + 1 of the Q part and of the dO part (rows 4 L .. 4 L + 3),
-    each lane fetching its chunk at its row's offset."""
-    out = info_slot(S_T1, rel)
-    out += [valu(f"v_add_u32 {vreg(V_IRO)}, {sreg(S_T1)}, {vreg(V_LRO)}", {f"s{S_T1}", f"v{V_LRO}"},
-                 {f"v{V_IRO}"})]
+def gather(slot, islot):
+    """This wave's share of a block's rows into ring slot `slot`, from the
+    row offsets in info slot `islot`: loads L = 2 w, 2 w + 1 of the Q part
+    and of the dO part (rows 4 L .. 4 L + 3), each lane fetching its chunk
+    at its row's offset."""
+    out = []
     for L in range(2):
-        out.append(Ins(f"ds_read_b32 {vreg(V_GT + L)}, {vreg(V_IRO)} offset:{16 * L}", "lds", {f"v{V_IRO}"},
-                       {f"v{V_GT + L}"}, lgkm=True))
+        out.append(Ins(f"ds_read_b32 {vreg(V_GT + L)}, {vreg(V_IRO)} offset:{1024 * islot + 16 * L}", "lds",
+                       {f"v{V_IRO}"}, {f"v{V_GT + L}"}, lgkm=True))
     for L in range(2):
         out.append(valu(f"v_add_u32 {vreg(V_GT + L)}, {vreg(V_GT + L)}, {vreg(V_CH + L)}",
                         {f"v{V_GT + L}", f"v{V_CH + L}"}, {f"v{V_GT + L}"}))
@@ -341,13 +330,11 @@ def gather(rel, slot):
     return out
 
 
-def mask_flag(rel):
-    """S_MNEXT = block r+rel has a row whose range does not hold every key of
-    the wave (from its bounds summary)."""
-    out = info_slot(S_T1, rel)
-    out += [valu(f"v_mov_b32 {vreg(V_FA)}, {sreg(S_T1)}", {f"s{S_T1}"}, {f"v{V_FA}"}),
-            Ins(f"ds_read_b64 {vreg(V_GT, 2)}, {vreg(V_FA)} offset:{4 * IW_MAXS}", "lds", {f"v{V_FA}"},
-                regs("v", V_GT, 2), lgkm=True),
+def mask_flag(islot):
+    """S_MNEXT = the block in info slot `islot` has a row whose range does
+    not hold every key of the wave (from its bounds summary)."""
+    return [Ins(f"ds_read_b64 {vreg(V_GT, 2)}, {vreg(V_FA)} offset:{1024 * islot + 4 * IW_MAXS}", "lds",
+                {f"v{V_FA}"}, regs("v", V_GT, 2), lgkm=True),
             valu(f"v_readfirstlane_b32 {sreg(S_T2)}, {vreg(V_GT)}", {f"v{V_GT}"}, {f"s{S_T2}"}),
             valu(f"v_readfirstlane_b32 {sreg(S_T3)}, {vreg(V_GT + 1)}", {f"v{V_GT + 1}"}, {f"s{S_T3}"}),
             Ins("s_nop 4", "nop"),
@@ -357,17 +344,17 @@ def mask_flag(rel):
             salu(f"s_cselect_b32 {sreg(S_T2)}, 1, 0", wr={f"s{S_T2}"}),
             salu(f"s_or_b32 {sreg(S_MNEXT)}, {sreg(S_MNEXT)}, {sreg(S_T2)}", {f"s{S_MNEXT}", f"s{S_T2}"},
                  {f"s{S_MNEXT}"})]
-    return out
 
 
 # ---------------------------------------------------------------------------
 # steps
 # ---------------------------------------------------------------------------
 # Step r (phase q): S(r+1), dP(r+1) from block r+1's rows in ring slot
-# (q+1) % 4, dV^T(r), dK^T(r) from block r's rows in slot q.  It gathers
-# block r+3 into slot (q+3) % 4 (block r-1's, last read by step r-1), loads
-# block r+5's info and reads block r+2's bounds summary for the next step's
-# mask choice.
+# (q+1) % 4, dV^T(r), dK^T(r) from block r's rows in slot q.  Block b's info
+# is in info slot b % 4.  The step first loads block r+4's info into info
+# slot q (block r's, last read by step r-1), then gathers block r+3 into
+# ring slot (q+3) % 4 (block r-1's, last read by step r-1) and reads block
+# r+2's bounds summary for the next step's mask choice.
 
 
 def _spread(items, nm, lo=0.1, hi=0.75):
@@ -402,10 +389,11 @@ def step_code(q, kind, masked):
         reads.setdefault(at, []).extend(load_ins(ld, o, q))
     side_extra = {}
     if kind != "last":
-        g = gather(3, (q + 3) % 4)
-        ip, ii = info_dma(5, split=True)
-        groups = [mask_flag(2), g[:9]] + [g[9 + 2 * k: 11 + 2 * k] for k in range(4)] + [ip, ii]
-        side_extra = _spread(groups, nm)
+        # the info load is this step's first memory operation (the next
+        # step's barrier waits for it and lets the four gathers run on)
+        g = gather((q + 3) % 4, (q + 3) % 4)
+        groups = [info_dma(4, q), mask_flag((q + 2) % 4), g[:4]] + [g[4 + 2 * k: 6 + 2 * k] for k in range(4)]
+        side_extra = _spread(groups, nm, 0.02, 0.6)
 
     def side(i):
         return side_extra.get(i, []) + reads.get(i, [])
@@ -415,9 +403,10 @@ def step_code(q, kind, masked):
         carried = packs(D_V, PD_V)           # dS(r), before dP(r+1) overwrites it
     vl = list(carried)
     if kind != "last":
+        islot = (q + 1) % 4
         if masked:
-            vl += mask()
-        vl += exps() + dss() + packs(S_V, PP_V)
+            vl += mask(islot)
+        vl += exps(islot) + dss(islot) + packs(S_V, PP_V)
     o, _ = schedule(mf, vl, side, carry=False, n_carried=len(carried), lead_cap=4, one_feed=True)
     return o
 
@@ -426,9 +415,10 @@ def step_blocks(tag, q, kind, end_label):
     u = "%="
     if kind == "pre":
         return [Block(f"L{tag}_a_{u}", step_code(q, "pre", True))]
-    # block r+1's rows (gathered two steps ago) have landed in every wave;
-    # the previous step's five loads may still be in flight
-    blocks = [Block(f"L{tag}_s_{u}", [waitcnt(vm=5, lgkm=0), Ins("s_barrier", "barrier")])]
+    # block r+1's rows (gathered two steps ago) have landed in every wave,
+    # and so has the info of block r+3 (the previous step's first load);
+    # the previous step's four gathers may still be in flight
+    blocks = [Block(f"L{tag}_s_{u}", [waitcnt(vm=4, lgkm=0), Ins("s_barrier", "barrier")])]
     if kind == "last":
         blocks.append(Block(f"L{tag}_a_{u}", step_code(q, "last", False)
                             + [branch("s_branch", end_label, cond=False)]))
@@ -491,8 +481,11 @@ def prologue():
     out += [valu(f"v_mov_b32 {vreg(V_CH + L)}, {vreg(S_V + 6 + L)}", {f"v{S_V + 6 + L}"}, {f"v{V_CH + L}"})
             for L in range(2)]
     out += [valu(f"v_mov_b32 {vreg(V_KEY)}, {vreg(S_V + 12)}", {f"v{S_V + 12}"}, {f"v{V_KEY}"}),
-            valu(f"v_mov_b32 {vreg(V_L16H)}, {vreg(S_V + 13)}", {f"v{S_V + 13}"}, {f"v{V_L16H}"}),
-            valu(f"v_mov_b32 {vreg(V_LRO)}, {vreg(S_V + 14)}", {f"v{S_V + 14}"}, {f"v{V_LRO}"})]
+            valu(f"v_add_u32 {vreg(V_ILH)}, {s_in('info0')}, {vreg(S_V + 13)}", {f"v{S_V + 13}"},
+                 {f"v{V_ILH}"}),
+            valu(f"v_add_u32 {vreg(V_IRO)}, {s_in('info0')}, {vreg(S_V + 14)}", {f"v{S_V + 14}"},
+                 {f"v{V_IRO}"}),
+            valu(f"v_mov_b32 {vreg(V_FA)}, {s_in('info0')}", set(), {f"v{V_FA}"})]
     for kk in range(8):
         out.append(valu(f"v_xor_b32 {vreg(AOFF_V + kk)}, {32 * kk}, {vreg(S_V + 4)}", {f"v{S_V + 4}"},
                         {f"v{AOFF_V + kk}"}))
@@ -504,25 +497,19 @@ def prologue():
     out += [valu(f"v_mov_b32 {vreg(z + k)}, 0", set(), {f"v{z + k}"}) for k in range(4)]
     for blk in range(16):
         out.append(mfma(("a", 16 * blk), ("v", z), ("v", z), False))
-    # info of blocks 0..3 (S_R1 = 0 here: list index r + rel with r = -1)
-    for b in range(4):
-        out += info_dma(b + 1)
-    # blocks 0-1's info has landed (this wave's own loads; 2-3 may still be
-    # in flight), and every wave has read its inputs
-    out += [waitcnt(vm=2, lgkm=0), Ins("s_barrier", "barrier")]
-    out += gather(1, 0) + gather(2, 1)
-    out += step_prefix(1)
-    out += mask_flag(2)
-    # block 0's rows have landed in every wave (block 1's four loads may
-    # still be in flight)
+    # info of blocks 0..2 into info slots 0..2 (S_R1 = 0 here: list index
+    # r + rel with r = -1)
+    for b in range(3):
+        out += info_dma(b + 1, b)
+    # blocks 0-1's info has landed (this wave's own loads; 2 may still be in
+    # flight), and every wave has read its inputs
+    out += [waitcnt(vm=1, lgkm=0), Ins("s_barrier", "barrier")]
+    out += gather(0, 0) + gather(1, 1)
+    out += mask_flag(1)
+    # block 0's rows have landed in every wave, and block 2's info (block
+    # 1's four gathers may still be in flight)
     out += [waitcnt(vm=4), Ins("s_barrier", "barrier")]
     return out
-
-
-def step_prefix(rel=1):
-    """The info read base (+ 16 hh) of block r+rel, r+1 = S_R1."""
-    return info_slot(S_INF, rel) + [valu(f"v_add_u32 {vreg(V_ILH)}, {sreg(S_INF)}, {vreg(V_L16H)}",
-                                         {f"s{S_INF}", f"v{V_L16H}"}, {f"v{V_ILH}"})]
 
 
 def epilogue():
@@ -557,12 +544,12 @@ def program():
     blocks = [Block(f"Lpro_{u}", prologue() + [salu(f"s_cmp_le_i32 {sreg(S_N)}, 0"),
                                                   branch("s_cbranch_scc1", f"Lepi_{u}")])]
     blocks += step_blocks("p", 3, "pre", None)
-    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R1)}, 1")] + step_prefix(1)))
+    blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R1)}, 1")]))
     for q in range(4):
         blocks.append(Block(f"Lt{q}_{u}", [salu(f"s_cmp_ge_i32 {sreg(S_R1)}, {sreg(S_N)}"),
                                           branch("s_cbranch_scc1", f"Llast{q}_{u}")]))
         blocks += step_blocks(f"f{q}", q, "full", f"Linc{q}_{u}")
-        tail = [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")] + step_prefix(1)
+        tail = [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")]
         if q == 3:
             tail.append(branch("s_branch", f"Lt0_{u}", cond=False))
         blocks.append(Block(f"Linc{q}_{u}", tail))
