@@ -21,14 +21,19 @@ a fixed register plus an immediate offset.  Four products per block,
 in the forms whose accumulators are the next products' B operands:
 
   S    = Q K^T       (A: Q rows from LDS, B: K in VGPRs; lane = key)
-  dP   = dO V^T      (A: dO rows from LDS, B: V rows from LDS)
+  D    = Delta - dO V^T   (A: dO rows from LDS, B: -V rows from LDS, C: Delta)
   dV^T += dO^T P     (A: dO^T by transposing LDS reads, B: P packed)
-  dK^T += Q^T dS     (A: Q^T by transposing LDS reads, B: dS packed)
+  -dK^T += Q^T (P D) (A: Q^T by transposing LDS reads, B: P D = -dS packed)
+
+Each wave negates its own V rows in LDS once (exact for bf16), and the dP
+accumulation starts from each row's Delta (the MFMA's C operand), so D =
+Delta - dP comes out of the matrix cores and -dS = P D costs one multiply;
+the epilogue scales dK^T by -scale.
 
 Step r (phase q = r mod 4) issues S(r+1), dP(r+1) (32 MFMAs), then
 dV^T(r), dK^T(r) (32 MFMAs).  Its VALU work: the packing of dS(r) (before
-dP(r+1) overwrites it), P = 2^(S c - LSE) and dS = P (dP - Delta) of block
-r+1 in place (after the masking of block r+1 when some row of it does not
+dP(r+1) overwrites it), P = 2^(S c - LSE) and -dS = P D of block r+1 in
+place (after the masking of block r+1 when some row of it does not
 see every key of the wave), and the packing of P(r+1) (after dV^T(r) has
 read P(r)).  It loads block r+4's info into info slot q and gathers block
 r+3's rows into ring slot (q+3) % 4.
@@ -38,12 +43,13 @@ Register map (per lane; j = key in the half, hh = lane / 32):
   a[128:255]  dV^T accumulators, likewise
   v[0:63]     K operands, (kh, kk) at 32 kh + 4 kk
   v[64:95]    S, kh at 64 + 16 kh (element e: row 8 (e >> 2) + 4 hh + (e & 3))
-  v[96:127]   dP, likewise (dS in place)
+  v[96:127]   D = Delta - dP, likewise (-dS in place)
   v[128:143]  P operands (bf16), (kh, s2) at 128 + 8 kh + 4 s2
-  v[144:159]  dS operands, likewise
-  v[160:191]  eight operand staging sets
-  v[192:255]  LDS addresses, LSE / Delta of four rows at a time, mask
-              temporaries, gather and store offsets
+  v[144:159]  -dS operands, likewise
+  v[160:183]  six operand staging sets
+  v[184:255]  LDS addresses, LSE of four rows at a time, Delta of the
+              block's rows (the C operand of D), mask temporaries, gather
+              and store offsets
 """
 
 from __future__ import annotations
@@ -63,13 +69,13 @@ DK_A, DV_A = 0, 128
 KB_V = 0
 S_V, D_V = 64, 96
 PP_V, PD_V = 128, 144
-ST_V, N_SETS = 160, 8
+ST_V, N_SETS = 160, 6
 LEADM = 4                 # MFMAs between an operand's read and the first MFMA that takes it
-AOFF_V = 192              # [kk] Q / dO row read address (ring slot 0, Q part)
-VOFF_V = 200              # [kk] V row read address (key half 0)
-TOFF_V = 208              # [db][a] transposing read address (ring slot 0, Q part, k-step 0)
-V_LSE = 216               # [j' % 2][e]: LSE of row 8 j' + 4 hh + e
-V_DLT = 224               # Delta, likewise
+AOFF_V = 184              # [kk] Q / dO row read address (ring slot 0, Q part)
+VOFF_V = 192              # [kk] V row read address (key half 0)
+TOFF_V = 200              # [db][a] transposing read address (ring slot 0, Q part, k-step 0)
+V_LSE = 208               # [j' % 2][e]: LSE of row 8 j' + 4 hh + e
+V_DC = 216                # [e]: Delta of row 8 (e >> 2) + 4 hh + (e & 3), the C operand of D
 V_IRO = 232               # info ring + this lane's gather row offsets (slot 0)
 V_ILH = 233               # info ring + 16 hh: this lane's rows (slot 0)
 V_CH = 234                # [L] chunk offset of this lane's gather load L
@@ -175,7 +181,14 @@ def mfma_ins(m):
         return mfma(("v", S_V + 16 * kh), ("v", st(a)), ("v", KB_V + 32 * kh + 4 * kk), kk > 0)
     if kind == "d":
         kk = idx
-        return mfma(("v", D_V + 16 * kh), ("v", st(a)), ("v", st(b)), kk > 0)
+        if kk > 0:
+            return mfma(("v", D_V + 16 * kh), ("v", st(a)), ("v", st(b)), True)
+        # the chain starts from Delta (C operand in its own registers)
+        dst, c = D_V + 16 * kh, V_DC
+        ab = regs("v", st(a), 4) | regs("v", st(b), 4)
+        return Ins(f"v_mfma_f32_32x32x16_bf16 {vreg(dst, 16)}, {vreg(st(a), 4)}, {vreg(st(b), 4)}, {vreg(c, 16)}",
+                   "mfma", ab | regs("v", c, 16), regs("v", dst, 16),
+                   mfma=(("v", dst), ab, regs("v", c, 16)))
     s2, db = idx
     if kind == "td":
         return mfma(("a", DV_A + 32 * db + 16 * kh), ("v", st(a)), ("v", PP_V + 8 * kh + 4 * s2), True)
@@ -212,19 +225,22 @@ def exps(slot):
     return out
 
 
-def dss(slot):
-    """dS = P (dP - Delta) in place in the dP registers."""
+def dss():
+    """-dS = P D = P (Delta - dP) in place in the D registers."""
     out = []
-    for jp in range(4):
-        out.append(row_read(V_DLT, IW_DLT, jp, slot))
-        for e in range(4 * jp, 4 * jp + 4):
-            for kh in range(2):
-                x = S_V + 16 * kh + e
-                d = D_V + 16 * kh + e
-                dl = V_DLT + 4 * (jp % 2) + (e & 3)
-                out.append(valu(f"v_sub_f32 {vreg(d)}, {vreg(d)}, {vreg(dl)}", {f"v{d}", f"v{dl}"}, {f"v{d}"}))
-                out.append(valu(f"v_mul_f32 {vreg(d)}, {vreg(d)}, {vreg(x)}", {f"v{d}", f"v{x}"}, {f"v{d}"}))
+    for e in range(16):
+        for kh in range(2):
+            x = S_V + 16 * kh + e
+            d = D_V + 16 * kh + e
+            out.append(valu(f"v_mul_f32 {vreg(d)}, {vreg(d)}, {vreg(x)}", {f"v{d}", f"v{x}"}, {f"v{d}"}))
     return out
+
+
+def delta_reads(slot):
+    """Delta of the block's rows into the C operand of D (element e = row
+    8 (e >> 2) + 4 hh + (e & 3)), from info slot `slot`."""
+    return [Ins(f"ds_read_b128 {vreg(V_DC + 4 * jp, 4)}, {vreg(V_ILH)} offset:{1024 * slot + 4 * IW_DLT + 32 * jp}",
+                "lds", {f"v{V_ILH}"}, regs("v", V_DC + 4 * jp, 4), lgkm=True) for jp in range(4)]
 
 
 def packs(src, dst):
@@ -400,13 +416,15 @@ def step_code(q, kind, masked):
 
     carried = []
     if kind != "pre":
-        carried = packs(D_V, PD_V)           # dS(r), before dP(r+1) overwrites it
+        carried = packs(D_V, PD_V)           # -dS(r), before D(r+1) overwrites it
+    if kind != "last":
+        carried += delta_reads((q + 1) % 4)  # block r+1's Delta, before D(r+1) starts from it
     vl = list(carried)
     if kind != "last":
         islot = (q + 1) % 4
         if masked:
             vl += mask(islot)
-        vl += exps(islot) + dss(islot) + packs(S_V, PP_V)
+        vl += exps(islot) + dss() + packs(S_V, PP_V)
     o, _ = schedule(mf, vl, side, carry=False, n_carried=len(carried), lead_cap=4, one_feed=True)
     return o
 
@@ -504,6 +522,18 @@ def prologue():
     # blocks 0-1's info has landed (this wave's own loads; 2 may still be in
     # flight), and every wave has read its inputs
     out += [waitcnt(vm=1, lgkm=0), Ins("s_barrier", "barrier")]
+    # -V: this wave's 64 V rows (the only ones it reads) negated in place,
+    # 16 bytes per lane and read
+    t2 = S_V + 16
+    out.append(valu(f"v_add_u32 {vreg(V_TMP)}, {s_in('vl')}, {vreg(V_L16)}", {f"v{V_L16}"}, {f"v{V_TMP}"}))
+    for i in range(16):
+        d = t2 + 4 * (i % 8)
+        out.append(Ins(f"ds_read_b128 {vreg(d, 4)}, {vreg(V_TMP)} offset:{1024 * i}", "lds", {f"v{V_TMP}"},
+                       regs("v", d, 4), lgkm=True))
+        for k in range(4):
+            out.append(valu(f"v_xor_b32 {vreg(d + k)}, 0x80008000, {vreg(d + k)}", {f"v{d + k}"}, {f"v{d + k}"}))
+        out.append(Ins(f"ds_write_b128 {vreg(V_TMP)}, {vreg(d, 4)} offset:{1024 * i}", "lds_w",
+                       {f"v{V_TMP}"} | regs("v", d, 4), set(), lgkm=True))
     out += gather(0, 0) + gather(1, 1)
     out += mask_flag(1)
     # block 0's rows have landed in every wave, and block 2's info (block
@@ -524,8 +554,9 @@ def epilogue():
                     a = acc + 32 * db + 16 * kh + k
                     out.append(valu(f"v_accvgpr_read_b32 {vreg(tv + k)}, {areg(a)}", {f"a{a}"}, {f"v{tv + k}"}))
                 if scl:
+                    # the loop accumulated -dK^T
                     for k in range(16):
-                        out.append(valu(f"v_mul_f32 {vreg(tv + k)}, {s_in('scale')}, {vreg(tv + k)}",
+                        out.append(valu(f"v_mul_f32 {vreg(tv + k)}, -{s_in('scale')}, {vreg(tv + k)}",
                                         {f"v{tv + k}"}, {f"v{tv + k}"}))
                 for jj in range(4):
                     for k in range(2):

@@ -4,10 +4,14 @@ against the oracle and against the eight-wave dK/dV kernel.
 The 64-key kernel is the default where the eight-wave kernel would not
 split its (key tile, KV head) pairs (512 pairs or more); SWATTN_DKDV_KERNEL
 =wide forces it (unsplit) on the small shapes of test_gpu_backward, =narrow
-forces the eight-wave kernel.  Both compute P = 2^(c s - LSE) and dS = P
-(dP - Delta) with the same fp32 operations, round them to bf16 the same way
-and accumulate in the same order, so where neither splits, their dk and dv
-must agree bit for bit.  The forced shapes cover single and partial tiles,
+forces the eight-wave kernel.  Both compute P = 2^(c s - LSE) with the same
+fp32 operations, round it to bf16 the same way and accumulate in the same
+order, so where neither splits their dv agrees bit for bit.  The 64-key
+kernel takes dP - Delta from the matrix cores (the accumulation starts
+from Delta, against negated V rows), the eight-wave kernel subtracts Delta
+afterwards: their fp32 roundings differ, so dk agrees to a bar of rel. L2
+2e-3 and max-abs 1e-2 of the largest element (a few bf16 ulps of dS on
+rows where dP and Delta nearly cancel), far inside the oracle bars.  The forced shapes cover single and partial tiles,
 G = 1 / 5 / 8, B > 1, Skv != Sq (key tiles past the last row, rows with no
 key), windows shorter than a tile (masked blocks), nearly one-hot and
 nearly uniform rows and packed sequences with metadata; each dk and dv is
@@ -91,16 +95,22 @@ def test_wide_dkdv_varlen_metadata(monkeypatch):
     (1, 8192, 16, 16, 512, 0.3),     # 32 key tiles x 16 KV heads = 512 pairs: no split
     (2, 4096, 32, 16, 300, 0.5),     # two sequences, 512 pairs
 ])
-def test_wide_dkdv_bit_identical_where_unsplit(monkeypatch, b, s, hq, hkv, w, p):
+def test_wide_dkdv_matches_eight_wave_where_unsplit(monkeypatch, b, s, hq, hkv, w, p):
     """Where the eight-wave kernel does not split, the default (64-key)
-    kernel's dk and dv equal it bit for bit, and reruns are bit-identical."""
+    kernel's dq and dv equal it bit for bit, its dk within the bar above,
+    and reruns are bit-identical."""
     q, k, v, do = _qkv(b * 7 + s, b, s, hq, hkv)
     m = _mask(s + 9, (b, s), p)
     wide = _run(q, k, v, do, m, w)
     again = _run(q, k, v, do, m, w)
     narrow = _forced(monkeypatch, "narrow", q, k, v, do, m, w)
     for name, a, c, n in zip(("dq", "dk", "dv"), wide, again, narrow):
-        diff = float((a.float() - n.float()).abs().max())
-        print(f"[wide dkdv] b{b} s{s} {name}: max |wide - narrow| = {diff:.3e}", flush=True)
+        a32, n32 = a.float(), n.float()
+        diff = float((a32 - n32).abs().max())
+        l2 = float((a32 - n32).norm() / n32.norm().clamp_min(1e-20))
+        print(f"[wide dkdv] b{b} s{s} {name}: max |wide - narrow| = {diff:.3e}, rel L2 {l2:.2e}", flush=True)
         assert torch.equal(a, c), f"{name}: reruns differ"
-        assert torch.equal(a, n), f"{name}: the 64-key and eight-wave kernels differ by {diff:.3e}"
+        if name == "dk":
+            assert l2 <= 2e-3 and diff <= 1e-2 * float(n32.abs().max()), f"dk: rel L2 {l2:.2e}, max {diff:.3e}"
+        else:
+            assert torch.equal(a, n), f"{name}: the 64-key and eight-wave kernels differ by {diff:.3e}"
