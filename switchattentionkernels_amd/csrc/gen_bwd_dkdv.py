@@ -301,13 +301,18 @@ def _mask_group(jp, slot):
 
 def block_index(sdst, rel):
     """sdst = packed block of list index a = min(r + rel, n - 1) (S_R1 = r
-    + 1): a + pb0 for a < n0, else a + pb1 (pb1 already less n0)."""
+    + 1).  The full-branch blocks come first, from the last down (pbf =
+    the last one's packed index), so that the pairs an XCD runs at once,
+    which share their full rows' later blocks, read the same block at about
+    the same time; then the local blocks from the first up: a + pb1 (pb1
+    already less n0; pb1n = pb1 + n0)."""
     return [salu(f"s_add_u32 {sreg(sdst)}, {sreg(S_R1)}, {rel - 1}"),
             salu(f"s_add_u32 {sreg(S_T3)}, {sreg(S_N)}, -1"),
             salu(f"s_min_i32 {sreg(sdst)}, {sreg(sdst)}, {sreg(S_T3)}"),
-            salu(f"s_cmp_lt_i32 {sreg(sdst)}, {s_in('n0')}"),
-            salu(f"s_cselect_b32 {sreg(S_T3)}, {s_in('pb0')}, {s_in('pb1')}"),
-            salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {sreg(S_T3)}")]
+            salu(f"s_sub_u32 {sreg(S_T3)}, {s_in('pbf')}, {sreg(sdst)}"),
+            salu(f"s_add_u32 {sreg(sdst)}, {sreg(sdst)}, {s_in('pb1')}"),
+            salu(f"s_cmp_lt_i32 {sreg(sdst)}, {s_in('pb1n')}"),
+            salu(f"s_cselect_b32 {sreg(sdst)}, {sreg(S_T3)}, {sreg(sdst)}")]
 
 
 def info_dma(rel, slot):

@@ -742,8 +742,8 @@ void bwd_dkdv_wide_kernel(const BwdParams p) {
                  [dkrsrc] "s"(dkrsrc), [dvrsrc] "s"(dvrsrc), [vbase] "s"(vb64),
                  [vbytes] "s"(__builtin_amdgcn_readfirstlane(vbytes)),
                  [nblk] "s"(__builtin_amdgcn_readfirstlane(nb)),
-                 [n0] "s"(__builtin_amdgcn_readfirstlane(n0)),
-                 [pb0] "s"(__builtin_amdgcn_readfirstlane(pb0)),
+                 [pb1n] "s"(__builtin_amdgcn_readfirstlane(pb1 + n0)),
+                 [pbf] "s"(__builtin_amdgcn_readfirstlane(pb0 + n0 - 1)),
                  [pb1] "s"(__builtin_amdgcn_readfirstlane(pb1)),
                  [kw0] "s"(__builtin_amdgcn_readfirstlane(kw0)),
                  [krow4] "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(4 * krowbytes))),
