@@ -37,7 +37,9 @@ The JSON line also carries:
 ``--configs cpu,b2,s16k,varlen,s64k,kvh1`` instead times the forward and the
 backward on each named workload (one JSON line each, no roofline);
 ``--p-sweep 0,0.1,0.25,0.5,1`` times config #3's attention call at each
-router density, beside the dense-causal call (one JSON line each).
+router density, beside the dense-causal call (one JSON line each); with
+``--power`` each call also loops for about 3 s while amd-smi samples the
+board power and the shader clock, and so does a register-only MFMA stream.
 """
 
 from __future__ import annotations
@@ -78,6 +80,10 @@ def parse():
     ap.add_argument("--p-sweep", default="",
                     help="comma-separated p_full values: config #3's attention call at each "
                          "router density (e.g. 0,0.1,0.25,0.5,1)")
+    ap.add_argument("--power", action="store_true",
+                    help="with --p-sweep: also loop each call for about 3 s while sampling the "
+                         "board power and the shader clock (amd-smi), and the same for a "
+                         "register-only MFMA stream")
     ap.add_argument("--configs", default="",
                     help="comma-separated workloads (cpu,b2,s16k,varlen,s64k): time the "
                          "forward and the backward on each once the clock has settled, one "
@@ -156,6 +162,75 @@ def config_table(args):
         torch.cuda.empty_cache()
 
 
+class PowerSampler:
+    """Board power (W) and mean shader clock (MHz) of GPU 0, sampled by
+    `amd-smi metric -p -c` in a thread about five times a second."""
+
+    def __init__(self):
+        import re
+        import shutil
+        import subprocess
+        import threading
+        self._re_p = re.compile(r"SOCKET_POWER:\s*([\d.]+)")
+        self._re_c = re.compile(r"GFX_\d+:\s*\n\s*CLK:\s*([\d.]+)")
+        self._cmd = ["amd-smi", "metric", "-p", "-c", "-g", "0"]
+        self._run = subprocess.run
+        self.samples = []
+        self._stop = threading.Event()
+        self._thread = None
+        if shutil.which("amd-smi"):
+            self._thread = threading.Thread(target=self._loop, daemon=True)
+            self._thread.start()
+
+    def _loop(self):
+        while not self._stop.is_set():
+            t = time.perf_counter()
+            try:
+                txt = self._run(self._cmd, capture_output=True, text=True, timeout=5).stdout
+            except Exception:  # sampling is diagnostic only
+                txt = ""
+            pw = self._re_p.search(txt)
+            clk = [float(x) for x in self._re_c.findall(txt)]
+            if pw and clk:
+                self.samples.append((t, float(pw.group(1)), sum(clk) / len(clk)))
+            self._stop.wait(0.2)
+
+    def mean(self, t0, t1):
+        sel = [(p, c) for t, p, c in self.samples if t0 <= t <= t1]
+        if not sel:
+            return None, None, 0
+        return (round(sum(p for p, _ in sel) / len(sel), 1), round(sum(c for _, c in sel) / len(sel)),
+                len(sel))
+
+    def stop(self):
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join(timeout=10)
+
+
+def _powered(sampler, fn, seconds=3.0, settle=1.0):
+    """Loop fn() for `seconds`; ms per call over the part after `settle`, with
+    the mean board power and clock sampled meanwhile."""
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < settle:
+        fn()
+        torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    n = 0
+    while time.perf_counter() - t0 < seconds - settle:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    e.record()
+    e.synchronize()
+    t1 = time.perf_counter()
+    pw, clk, ns = sampler.mean(t0, t1)
+    return s.elapsed_time(e) / n, pw, clk, ns
+
+
 def p_sweep(args):
     """Config #3 (s16k) over router densities: the swattn_prefill_fwd call
     (vt_pack_kernel + the attention kernel) timed on its stream once the clock has
@@ -168,6 +243,7 @@ def p_sweep(args):
     L = _lib.lib()
     stream = _lib.stream_handle(dev)
     dense_ms = None
+    sampler = PowerSampler() if args.power else None
     for p in [float(x) for x in args.p_sweep.split(",")]:
         wl = workloads.build("s16k", seed=args.seed, p_full=p)
         d = wl["workload"]
@@ -196,17 +272,39 @@ def p_sweep(args):
         flops = routed_flops(full, local, batch=B, seq_q=S, seq_kv=S, heads_q=HQ, head_dim=128,
                              window=W)
         ms = settled_ms(lambda: attn(full, local))
-        print(json.dumps({
+        line = {
             "p_sweep": p, "workload": f"s16k: B{B} S{S} Hq{HQ}/Hkv{HKV} d128 W{W} Bernoulli "
                                       f"p_full={p}, seed {args.seed}",
             "full_rows": int(full.numel()), "routed_gflop": round(flops / 1e9, 2),
             "entry_point_ms": round(ms, 4), "tflops": round(flops / ms / 1e9, 1),
             "frac_of_peak": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
             "routed_flop_fraction": round(flops / dense_flops, 4),
-            "routed_over_dense_time": round(ms / dense_ms, 4), "dense_ms": round(dense_ms, 4)}),
-            flush=True)
+            "routed_over_dense_time": round(ms / dense_ms, 4), "dense_ms": round(dense_ms, 4)}
+        if sampler is not None:
+            pms, pw, clk, ns = _powered(sampler, lambda: attn(full, local))
+            line.update({"powered_ms": round(pms, 4), "board_power_w": pw, "gfx_clock_mhz": clk,
+                         "power_samples": ns})
+        print(json.dumps(line), flush=True)
         del q, k, v, m, out, lse, ws, full, local
         torch.cuda.empty_cache()
+    if sampler is not None:
+        # The same for a register-only MFMA stream (two waves per SIMD).
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        blocks, iters = 2 * cus, 20000
+        probe = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+        P = _lib.probe_lib()
+
+        def peak():
+            st = P.swattn_mfma_peak(iters, blocks, probe.data_ptr(), stream)
+            if st != 0:
+                raise RuntimeError(f"swattn_mfma_peak failed with status {st}")
+
+        pms, pw, clk, ns = _powered(sampler, peak)
+        print(json.dumps({"power_probe": "register-only bf16 MFMA stream",
+                          "tflops": round(blocks * 4 * iters * 8 * 32768 / (pms * 1e-3) / 1e12, 1),
+                          "board_power_w": pw, "gfx_clock_mhz": clk, "power_samples": ns}),
+              flush=True)
+        sampler.stop()
 
 
 def _cpu_model() -> str:
