@@ -70,7 +70,7 @@ KB_V = 0
 S_V, D_V = 64, 96
 PP_V, PD_V = 128, 144
 ST_V, N_SETS = 160, 6
-LEADM = 4                 # MFMAs between an operand's read and the first MFMA that takes it
+LEADM = 2                 # MFMAs between an operand's read and the first MFMA that takes it
 AOFF_V = 184              # [kk] Q / dO row read address (ring slot 0, Q part)
 VOFF_V = 192              # [kk] V row read address (key half 0)
 TOFF_V = 200              # [db][a] transposing read address (ring slot 0, Q part, k-step 0)
