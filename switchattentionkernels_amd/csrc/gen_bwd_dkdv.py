@@ -12,9 +12,11 @@ Layout.  A workgroup owns a (256-key tile, KV head) pair: four waves of 64
 keys (two 32-key halves "kh"), one wave per SIMD.  The dK^T and dV^T
 accumulators (128 d x 64 keys each, fp32) fill the 256 AGPRs; the wave's K
 rows (the B operands of S) sit in 64 VGPRs; the tile's V rows sit in LDS.
-The 32-row blocks of rows that can see the tile stream through a four-slot
-LDS ring (Q block, dO block), gathered from the rows' positions by 32-bit
-buffer offsets that bwd_prep_kernel writes into each block's 1 KiB info;
+The 32-row blocks of rows that can see the tile (the full-branch blocks
+from the last down, then the local ones from the first up) stream through
+a four-slot LDS ring (Q block, dO block), gathered from the rows' positions
+by 32-bit buffer offsets that bwd_prep_kernel writes into each block's
+1 KiB info;
 the info blocks (LSE, Delta, key bounds, row offsets) travel through a
 four-slot ring, each wave loading its own copy, so that every info read is
 a fixed register plus an immediate offset.  Four products per block,
