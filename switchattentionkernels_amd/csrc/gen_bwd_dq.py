@@ -18,7 +18,8 @@ cores read and accumulate there directly), S, dP and everything else the
 the accumulators of one are the B operands of the next:
 
   S^T  = K Q^T      (A: K rows from LDS, B: Q^T in AGPRs)
-  dP^T = V dO^T     (A: V rows from LDS, B: dO^T in AGPRs)
+  D    = V dO^T - Delta  (A: V rows from LDS, B: dO^T in AGPRs, starting
+                     from -Delta of each row, moved in before the MFMAs)
   dQ^T += K^T dS^T  (A: K^T by transposing LDS reads of the same K tile,
                      B: dS^T packed to bf16 from the S accumulators)
 
@@ -34,8 +35,9 @@ that the scores of tile r+1 are complete early and their exponentials can
 spread over the rest of the step.  Its VALU work: dS of tile r's keys 32-63
 and their packing (before the dQ^T MFMAs that read them), P = 2^(S c -
 LSE) of tile r+1 (after the masking of tile r+1 when it lies outside the
-range every row of the wave covers), dS of tile r+1's keys 0-31 and their
-packing.  A list scheduler spreads it over the MFMA slots, at most one
+range every row of the wave covers), dS = P D (one multiply per element) of
+tile r+1's keys 0-31 and their packing, and the -Delta starting values of
+the dP^T accumulators of tile r+1.  A list scheduler spreads it over the MFMA slots, at most one
 exponential and one instruction feeding an exponential per slot.  K and V tiles stream through four-slot LDS rings, staged by the
 four waves with global -> LDS loads three (K) and four (V) steps ahead;
 the loop is unrolled four steps so that every LDS address is a base
@@ -48,10 +50,11 @@ Register map (per lane; "rb" = 32-row block of the wave's 64 rows, "h" =
   a[192:255]  dO^T operands, likewise
   v[0:63], v[64:127]  S tiles (ping-pong), (rb, h) at +32 rb + 16 h; after
               the packing, dS^T operand (k-step s2, rb) at +8 s2 + 4 rb
-  v[128:191]  dP^T tile, same layout
+  v[128:191]  dP^T - Delta tile, same layout
   v[192:207]  four operand staging sets
   v[208:255]  LDS addresses, row state, mask temporaries, DMA and store
-              offsets
+              offsets; (-Delta, -Delta) of row block 0 at 234-235 and of
+              row block 1 at 254-255
 """
 
 from __future__ import annotations
@@ -77,7 +80,7 @@ KOFF_V = 208                 # [kk] K row read address (ring slot 0)
 VOFF_V = 216                 # [kk] V row read address (ring slot 0)
 TOFF_V = 224                 # [db][a] transposing read address (ring slot 0, k-step 0)
 V_NLSE = 232                 # [rb] -LSE
-V_DLT = 234                  # [rb] Delta
+V_DLT = 234                  # [rb] Delta (the prologue turns 234-235 into V_NDLT[0])
 V_KSR = 236                  # [rb] row start - 4 hh
 V_SPAN = 238                 # [rb] row key count
 V_LO = 240                   # [rb] mask: row start - 4 hh - first key of the tile
@@ -87,6 +90,7 @@ V_TMP = 247
 V_KDMA = 248                 # [i] global offsets of this lane's K / V DMA loads
 V_DQOFF = 252                # [rb] dq row byte offset (+ 8 hh); 254, 255: Q row offsets (prologue)
 V_QOFF = 254
+V_NDLT = (234, 254)          # [rb] (-Delta, -Delta) register pairs, the loop's dP^T starting values
 
 S_T0, S_T1 = 52, 53
 S_R1 = 54                    # r + 1 for step r (the tile whose S and dP the step computes)
@@ -148,7 +152,8 @@ def op_mfmas(op, o, sc, sn):
     if kind == "k":
         return [mfma(("v", sn + 32 * rb + 16 * a), src, ("a", Q_A + 8 * b + 4 * rb), b > 0) for rb in range(2)]
     if kind == "v":
-        return [mfma(("v", D_V + 32 * rb + 16 * a), src, ("a", DO_A + 8 * b + 4 * rb), b > 0) for rb in range(2)]
+        # accumulates onto -Delta (prefill): the result is dP^T - Delta
+        return [mfma(("v", D_V + 32 * rb + 16 * a), src, ("a", DO_A + 8 * b + 4 * rb), True) for rb in range(2)]
     return [mfma(("a", DQ_A + 32 * b + 16 * rb), src, ("v", sc + 8 * a + 4 * rb), True) for rb in range(2)]
 
 
@@ -198,13 +203,26 @@ def exps(s, h):
     return out
 
 
+def prefill(h):
+    """The dP^T accumulators of half h start from -Delta of their row (eight
+    64-bit moves per row block from its (-Delta, -Delta) pair), so that the
+    MFMAs leave dP^T - Delta there."""
+    out = []
+    for rb in range(2):
+        base = D_V + 32 * rb + 16 * h
+        pr = V_NDLT[rb]
+        for i in range(0, 16, 2):
+            out.append(valu(f"v_mov_b64 {vreg(base + i, 2)}, {vreg(pr, 2)}", {f"v{pr}", f"v{pr + 1}"},
+                            {f"v{base + i}", f"v{base + i + 1}"}))
+    return out
+
+
 def dss(s, h):
-    """dS = P (dP - Delta) in place for half h (dP - Delta in place in D)."""
+    """dS = P (dP - Delta) in place for half h (dP - Delta is what the dP^T
+    MFMAs left in D)."""
     out = []
     for rb, x in half_elems(s, h):
         d = D_V + (x - s)
-        out.append(valu(f"v_sub_f32 {vreg(d)}, {vreg(d)}, {vreg(V_DLT + rb)}", {f"v{d}", f"v{V_DLT + rb}"},
-                        {f"v{d}"}))
         out.append(valu(f"v_mul_f32 {vreg(x)}, {vreg(x)}, {vreg(d)}", {f"v{x}", f"v{d}"}, {f"v{x}"}))
     return out
 
@@ -303,6 +321,10 @@ def step_code(q, kind, masked):
     carried = []
     if kind != "pre":
         carried = dss(sc, 1) + packs(sc, 1)
+    if kind != "last":
+        # carried work goes before the first MFMA that touches its
+        # registers: here the dP^T MFMAs that accumulate onto it
+        carried += prefill(0) + prefill(1)
     vl = list(carried)
     if kind != "last":
         pre_mask = []
@@ -409,6 +431,13 @@ def prologue():
     # Q, dO, K(0) and V(0) have landed in every wave, and every wave has
     # read its inputs (V slot 3 is staged into by the pre step)
     out += [waitcnt(vm=12, lgkm=0), Ins("s_barrier", "barrier")]
+    # The (-Delta, -Delta) pairs, row block 1's on the Q offsets, free now
+    # that the Q / dO rows have landed.
+    n0, n1 = V_NDLT
+    out += [valu(f"v_xor_b32 {vreg(n1)}, 0x80000000, {vreg(V_DLT + 1)}", {f"v{V_DLT + 1}"}, {f"v{n1}"}),
+            valu(f"v_xor_b32 {vreg(n1 + 1)}, 0x80000000, {vreg(V_DLT + 1)}", {f"v{V_DLT + 1}"}, {f"v{n1 + 1}"}),
+            valu(f"v_xor_b32 {vreg(n0)}, 0x80000000, {vreg(V_DLT)}", {f"v{V_DLT}"}, {f"v{n0}"}),
+            valu(f"v_mov_b32 {vreg(n0 + 1)}, {vreg(n0)}", {f"v{n0}"}, {f"v{n0 + 1}"})]
     return out
 
 

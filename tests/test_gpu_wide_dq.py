@@ -1,10 +1,13 @@
 """The backward's 256-row dQ kernel (bwd_dq_wide_kernel, the default) against
 the 32-row-wave dQ kernel (SWATTN_DQ_KERNEL=narrow) and the oracle.
 
-Both kernels compute P = 2^(c s - LSE) and dS = P (dP - Delta) with the same
-fp32 operations, round dS to bf16 the same way and accumulate S, dP and dQ
-in the same k-step order, so their dq must agree bit for bit; dk and dv come
-from the same kernel either way.  The shapes cover single and partial tiles,
+Both kernels compute P = 2^(c s - LSE) with the same fp32 operations and
+accumulate S and dQ in the same k-step order.  The 256-row kernel starts
+its dP accumulation from -Delta (so the matrix cores return dP - Delta)
+where the 32-row-wave kernel subtracts Delta afterwards: their dS differ
+in rounding only, and so their dq agree to rel. L2 2e-3 and 1 % of the
+largest element; dk and dv come from the same kernel either way and agree
+bit for bit.  The shapes cover single and partial tiles,
 G = 1 / 5 / 8, B > 1, Skv != Sq, rows with no key (dq = 0), windows shorter
 than a tile or starting inside one (masked tiles), nearly one-hot and nearly
 uniform rows, packed sequences with metadata, and row tiles cut into pieces
@@ -34,9 +37,15 @@ def _both(monkeypatch, *args, **kw):
 
 def _same(wide, narrow, tag):
     for name, a, b in zip(("dq", "dk", "dv"), wide, narrow):
-        diff = float((a.float() - b.float()).abs().max()) if a.numel() else 0.0
-        print(f"[wide dq] {tag} {name}: max |wide - narrow| = {diff:.3e}", flush=True)
-        assert torch.equal(a, b), f"{tag} {name}: wide and narrow dQ kernels differ by {diff:.3e}"
+        a32, b32 = a.float(), b.float()
+        diff = float((a32 - b32).abs().max()) if a.numel() else 0.0
+        l2 = float((a32 - b32).norm() / b32.norm().clamp_min(1e-20)) if a.numel() else 0.0
+        print(f"[wide dq] {tag} {name}: max |wide - narrow| = {diff:.3e}, rel L2 {l2:.2e}", flush=True)
+        if name == "dq":
+            big = float(b32.abs().max()) if b.numel() else 0.0
+            assert l2 <= 2e-3 and diff <= 1e-2 * big, f"{tag} dq: rel L2 {l2:.2e}, max {diff:.3e}"
+        else:
+            assert torch.equal(a, b), f"{tag} {name}: the two runs differ by {diff:.3e}"
 
 
 @pytest.mark.parametrize("b,s,hq,hkv,w,p,skv", [
