@@ -112,6 +112,9 @@ LDS_BYTES = 2 * V_RING
 # lane, 1 KiB per group and wave; waves 0-1 in K slot 3, waves 2-3 in V slot
 # 3 (slots the prologue does not stage into).
 AUX_GROUPS = 7
+# Per-wave staging of the dq rows in the epilogue (in K slots 0-2, free
+# after the loop): 32 rows at a 272-byte stride, then their byte offsets.
+EPI_REGION = 32 * 272 + 128
 
 
 # ---------------------------------------------------------------------------
@@ -442,33 +445,77 @@ def prologue():
 
 
 def epilogue():
-    """dq rows: scale * dQ^T as bf16, four values (8 bytes) per store; or,
-    for a piece of a cut row tile, the fp32 partial as sixteen float4 units
-    per lane and row block: unit 4 db + j at (16 rb + unit) KiB + 16 lane of
-    the wave's part.  Returns the head (wait, branch to the piece stores),
-    the whole-row stores and the piece stores."""
+    """dq rows: scale * dQ^T as bf16, staged per 32-row block through this
+    wave's LDS region (rows at a 272-byte stride, then their byte offsets)
+    so that each store writes 16 bytes of a whole 256-byte row; or, for a
+    piece of a cut row tile, the fp32 partial as sixteen float4 units per
+    lane and row block: unit 4 db + j at (16 rb + unit) KiB + 16 lane of the
+    wave's part.  Returns the head (wait, branch to the piece stores), the
+    whole-row stores and the piece stores."""
     u = "%="
     head = [waitcnt(vm=0, lgkm=0), salu(f"s_cmp_lg_u32 {s_in('piece')}, 0"),
             branch("s_cbranch_scc1", f"Lpart_{u}")]
-    whole = []
+    # every wave is past its last LDS read of the rings
+    whole = [Ins("s_barrier", "barrier")]
+    E, t5, t6, lane = 184, 189, 190, 191      # v[184:191]: addresses (the loop's dP^T tile is dead)
+    whole += [
+        valu(f"v_mbcnt_lo_u32_b32 {vreg(lane)}, -1, 0", set(), {f"v{lane}"}),
+        valu(f"v_mbcnt_hi_u32_b32 {vreg(lane)}, -1, {vreg(lane)}", {f"v{lane}"}, {f"v{lane}"}),
+        # E: write base (row lane & 31, 8 bytes per lane half); E+1: this
+        # row's slot of the offset table; E+2: read base (row lane >> 4,
+        # 16-byte chunk lane & 15); E+3: offset-table read base; E+4: 16 (lane & 15)
+        valu(f"v_and_b32 {vreg(t5)}, 31, {vreg(lane)}", {f"v{lane}"}, {f"v{t5}"}),
+        valu(f"v_lshrrev_b32 {vreg(t6)}, 5, {vreg(lane)}", {f"v{lane}"}, {f"v{t6}"}),
+        valu(f"v_mul_u32_u24 {vreg(E)}, 0x110, {vreg(t5)}", {f"v{t5}"}, {f"v{E}"}),
+        valu(f"v_lshl_add_u32 {vreg(E)}, {vreg(t6)}, 3, {vreg(E)}", {f"v{t6}", f"v{E}"}, {f"v{E}"}),
+        valu(f"v_add_u32 {vreg(E)}, {s_in('ebase')}, {vreg(E)}", {f"v{E}"}, {f"v{E}"}),
+        valu(f"v_lshl_add_u32 {vreg(E + 1)}, {vreg(t5)}, 2, {s_in('ebase')}", {f"v{t5}"}, {f"v{E + 1}"}),
+        valu(f"v_add_u32 {vreg(E + 1)}, {32 * 272}, {vreg(E + 1)}", {f"v{E + 1}"}, {f"v{E + 1}"}),
+        valu(f"v_lshrrev_b32 {vreg(t6)}, 4, {vreg(lane)}", {f"v{lane}"}, {f"v{t6}"}),
+        valu(f"v_and_b32 {vreg(E + 4)}, 15, {vreg(lane)}", {f"v{lane}"}, {f"v{E + 4}"}),
+        valu(f"v_lshlrev_b32 {vreg(E + 4)}, 4, {vreg(E + 4)}", {f"v{E + 4}"}, {f"v{E + 4}"}),
+        valu(f"v_mul_u32_u24 {vreg(E + 2)}, 0x110, {vreg(t6)}", {f"v{t6}"}, {f"v{E + 2}"}),
+        valu(f"v_add3_u32 {vreg(E + 2)}, {s_in('ebase')}, {vreg(E + 2)}, {vreg(E + 4)}",
+             {f"v{E + 2}", f"v{E + 4}"}, {f"v{E + 2}"}),
+        valu(f"v_lshl_add_u32 {vreg(E + 3)}, {vreg(t6)}, 2, {s_in('ebase')}", {f"v{t6}"}, {f"v{E + 3}"}),
+        valu(f"v_add_u32 {vreg(E + 3)}, {32 * 272}, {vreg(E + 3)}", {f"v{E + 3}"}, {f"v{E + 3}"}),
+    ]
     for rb in range(2):
+        if rb == 1:
+            whole.append(waitcnt(lgkm=0))     # row block 0's reads of the region are done
         for db in range(4):
-            tv = 32 * (2 * rb + (db % 2)) + 16 * (db // 2)   # a 16-register block of v[0:127]
-            for k in range(16):
-                a = DQ_A + 32 * db + 16 * rb + k
-                whole.append(valu(f"v_accvgpr_read_b32 {vreg(tv + k)}, {areg(a)}", {f"a{a}"}, {f"v{tv + k}"}))
-            for k in range(16):
-                whole.append(valu(f"v_mul_f32 {vreg(tv + k)}, {s_in('scale')}, {vreg(tv + k)}", {f"v{tv + k}"},
-                                  {f"v{tv + k}"}))
             for j in range(4):
-                for k in range(2):
-                    whole.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 4 * j + k)}, {vreg(tv + 4 * j + 2 * k)}, "
-                                      f"{vreg(tv + 4 * j + 2 * k + 1)}",
-                                      {f"v{tv + 4 * j + 2 * k}", f"v{tv + 4 * j + 2 * k + 1}"},
-                                      {f"v{tv + 4 * j + k}"}))
-                whole.append(Ins(f"buffer_store_dwordx2 {vreg(tv + 4 * j, 2)}, {vreg(V_DQOFF + rb)}, "
-                                 f"{s_in('dqrsrc')}, 0 offen offset:{64 * db + 16 * j}", "vmem_st",
-                                 regs("v", tv + 4 * j, 2) | {f"v{V_DQOFF + rb}"}, set(), vm=True))
+                a0 = DQ_A + 32 * db + 16 * rb + 4 * j
+                tv = 8 * (4 * db + j) % 64   # rotate through v[0:63]
+                for k in range(4):
+                    whole.append(valu(f"v_accvgpr_read_b32 {vreg(tv + k)}, {areg(a0 + k)}", {f"a{a0 + k}"},
+                                      {f"v{tv + k}"}))
+                for k in range(4):
+                    whole.append(valu(f"v_mul_f32 {vreg(tv + k)}, {s_in('scale')}, {vreg(tv + k)}",
+                                      {f"v{tv + k}"}, {f"v{tv + k}"}))
+                whole.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 4)}, {vreg(tv)}, {vreg(tv + 1)}",
+                                  {f"v{tv}", f"v{tv + 1}"}, {f"v{tv + 4}"}))
+                whole.append(valu(f"v_cvt_pk_bf16_f32 {vreg(tv + 5)}, {vreg(tv + 2)}, {vreg(tv + 3)}",
+                                  {f"v{tv + 2}", f"v{tv + 3}"}, {f"v{tv + 5}"}))
+                whole.append(Ins(f"ds_write_b64 {vreg(E)}, {vreg(tv + 4, 2)} offset:{64 * db + 16 * j}",
+                                 "lds_w", {f"v{E}", f"v{tv + 4}", f"v{tv + 5}"}, set(), lgkm=True))
+        # the row's byte offset (its lane-half term cleared; a row not
+        # stored has an offset past the descriptor's range)
+        whole.append(valu(f"v_and_b32 {vreg(t5)}, 0xfffffff7, {vreg(V_DQOFF + rb)}", {f"v{V_DQOFF + rb}"},
+                          {f"v{t5}"}))
+        whole.append(Ins(f"ds_write_b32 {vreg(E + 1)}, {vreg(t5)}", "lds_w", {f"v{E + 1}", f"v{t5}"}, set(),
+                         lgkm=True))
+        whole.append(waitcnt(lgkm=0))
+        for i in range(8):
+            whole.append(Ins(f"ds_read_b32 {vreg(64 + i)}, {vreg(E + 3)} offset:{16 * i}", "lds",
+                             {f"v{E + 3}"}, {f"v{64 + i}"}, lgkm=True))
+            whole.append(Ins(f"ds_read_b128 {vreg(72 + 4 * i, 4)}, {vreg(E + 2)} offset:{4 * 272 * i}", "lds",
+                             {f"v{E + 2}"}, regs("v", 72 + 4 * i, 4), lgkm=True))
+        for i in range(8):
+            whole.append(valu(f"v_add_u32 {vreg(64 + i)}, {vreg(64 + i)}, {vreg(E + 4)}",
+                              {f"v{64 + i}", f"v{E + 4}"}, {f"v{64 + i}"}))
+            whole.append(Ins(f"buffer_store_dwordx4 {vreg(72 + 4 * i, 4)}, {vreg(64 + i)}, {s_in('dqrsrc')}, 0 "
+                             f"offen", "vmem_st", regs("v", 72 + 4 * i, 4) | {f"v{64 + i}"}, set(), vm=True))
     whole.append(branch("s_branch", f"Lend_{u}", cond=False))
     t = V_TMP
     part = [valu(f"v_mbcnt_lo_u32_b32 {vreg(t)}, -1, 0", set(), {f"v{t}"}),
@@ -547,6 +594,7 @@ def emit(path):
         f.write('  ""\n')
         f.write(f"#define SWATTN_BWD_DQ_LDS_BYTES {LDS_BYTES}\n")
         f.write(f"#define SWATTN_BWD_DQ_AUX_GROUPS {AUX_GROUPS}\n")
+        f.write(f"#define SWATTN_BWD_DQ_EPI_REGION {EPI_REGION}\n")
         f.write("#define SWATTN_BWD_DQ_CLOBBERS \\\n  ")
         f.write(", ".join(f'"{x}"' for x in clobbers()))
         f.write("\n")

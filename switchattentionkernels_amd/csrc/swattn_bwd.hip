@@ -1063,6 +1063,7 @@ __global__ __attribute__((amdgpu_flat_work_group_size(kBwdThreads, kBwdThreads),
 constexpr int kDqWideLdsBytes = SWATTN_BWD_DQ_LDS_BYTES;
 static_assert(kDqWideLdsBytes == 8 * kTileBytes, "four-slot K and V rings of the generated loop");
 constexpr int kDqAuxGroups = SWATTN_BWD_DQ_AUX_GROUPS;
+static_assert(4 * SWATTN_BWD_DQ_EPI_REGION <= 3 * kTileBytes, "the dq staging fits in K slots 0-2");
 // Per-lane inputs: group g of wave w at aux(w) + 1024 g + 16 lane, with
 // aux(w) in K slot 3 (waves 0-1) or V slot 3 (waves 2-3).
 __device__ __forceinline__ int dq_aux_offset(int wave) {
@@ -1246,6 +1247,7 @@ void bwd_dq_wide_kernel(const BwdParams p) {
                  [it1] "s"(__builtin_amdgcn_readfirstlane(it1)), [c] "s"(c), [scale] "s"(scale),
                  [ldsw] "s"(__builtin_amdgcn_readfirstlane(lds0 + wave * 4096)),
                  [aux] "s"(__builtin_amdgcn_readfirstlane(lds0 + dq_aux_offset(wave))),
+                 [ebase] "s"(__builtin_amdgcn_readfirstlane(lds0 + wave * SWATTN_BWD_DQ_EPI_REGION)),
                  [piece] "s"(__builtin_amdgcn_readfirstlane(piece ? 1 : 0))
                : SWATTN_BWD_DQ_CLOBBERS);
 }
