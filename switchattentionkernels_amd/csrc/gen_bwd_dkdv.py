@@ -551,8 +551,48 @@ def prologue():
 
 def epilogue():
     """dK = scale dK^T and dV = dV^T as bf16 rows, four values per store, at
-    each lane's key row (keys past the end fall outside the descriptors)."""
-    out = [waitcnt(vm=0, lgkm=0)]
+    each lane's key row (keys past the end fall outside the descriptors); or,
+    for one split of a pair's row blocks, the fp32 partials for
+    bwd_dkdv_reduce_kernel: key half kh of the wave is the reduce's wave
+    2 w + kh, dK^T block db elements 4 j .. 4 j + 3 its unit 4 db + j (with
+    the sign of dS^T Q: the loop accumulated its negative) and dV^T's unit
+    16 + 4 db + j, at (32 kh + unit) KiB + 16 lane of the wave's part.
+    Returns the head (wait, branch to the partial stores), the row stores
+    and the partial stores."""
+    u = "%="
+    head = [waitcnt(vm=0, lgkm=0), salu(f"s_cmp_lg_u32 {s_in('split')}, 0"),
+            branch("s_cbranch_scc1", f"Lpart_{u}")]
+    part = [valu(f"v_mbcnt_lo_u32_b32 {vreg(V_TMP)}, -1, 0", set(), {f"v{V_TMP}"}),
+            valu(f"v_mbcnt_hi_u32_b32 {vreg(V_TMP)}, -1, {vreg(V_TMP)}", {f"v{V_TMP}"}, {f"v{V_TMP}"}),
+            valu(f"v_lshlrev_b32 {vreg(V_TMP)}, 4, {vreg(V_TMP)}", {f"v{V_TMP}"}, {f"v{V_TMP}"})]
+    for kh in range(2):
+        for g in range(8):
+            vo = 8 * kh + g      # v[0:15]: lane offsets of unit group g of key half kh
+            part.append(valu(f"v_add_u32 {vreg(vo)}, {32768 * kh + 4096 * g}, {vreg(V_TMP)}", {f"v{V_TMP}"},
+                             {f"v{vo}"}))
+    for kh in range(2):
+        for db in range(4):
+            for j in range(4):
+                unit = 4 * db + j
+                a = DK_A + 32 * db + 16 * kh + 4 * j
+                t = 16 + 4 * ((4 * db + j) % 8)
+                for k in range(4):
+                    part.append(valu(f"v_accvgpr_read_b32 {vreg(t + k)}, {areg(a + k)}", {f"a{a + k}"},
+                                     {f"v{t + k}"}))
+                for k in range(4):
+                    part.append(valu(f"v_xor_b32 {vreg(t + k)}, 0x80000000, {vreg(t + k)}", {f"v{t + k}"},
+                                     {f"v{t + k}"}))
+                vo = 8 * kh + unit // 4
+                part.append(Ins(f"buffer_store_dwordx4 {vreg(t, 4)}, {vreg(vo)}, {s_in('prsrc')}, 0 offen "
+                                f"offset:{1024 * (unit % 4)}", "vmem_st", regs("v", t, 4) | {f"v{vo}"}, set(),
+                                vm=True))
+                unit = 16 + 4 * db + j
+                a = DV_A + 32 * db + 16 * kh + 4 * j
+                vo = 8 * kh + unit // 4
+                part.append(Ins(f"buffer_store_dwordx4 {areg(a, 4)}, {vreg(vo)}, {s_in('prsrc')}, 0 offen "
+                                f"offset:{1024 * (unit % 4)}", "vmem_st", regs("a", a, 4) | {f"v{vo}"}, set(),
+                                vm=True))
+    out = []
     for acc, rs, scl in ((DK_A, "dkrsrc", True), (DV_A, "dvrsrc", False)):
         for kh in range(2):
             for db in range(4):
@@ -574,7 +614,8 @@ def epilogue():
                     out.append(Ins(f"buffer_store_dwordx2 {vreg(tv + 4 * jj, 2)}, {vreg(V_DKOFF + kh)}, "
                                    f"{s_in(rs)}, 0 offen offset:{64 * db + 16 * jj}", "vmem_st",
                                    regs("v", tv + 4 * jj, 2) | {f"v{V_DKOFF + kh}"}, set(), vm=True))
-    return out
+    out.append(branch("s_branch", f"Lend_{u}", cond=False))
+    return head, out, part
 
 
 def program():
@@ -595,7 +636,9 @@ def program():
         bl = step_blocks(f"l{q}", q, "last", f"Lepi_{u}")
         bl[0].name = f"Llast{q}_{u}"
         blocks += bl
-    blocks.append(Block(f"Lepi_{u}", epilogue()))
+    head, whole, part = epilogue()
+    blocks += [Block(f"Lepi_{u}", head), Block(f"Lwhole_{u}", whole), Block(f"Lpart_{u}", part),
+               Block(f"Lend_{u}", [])]
     return blocks
 
 

@@ -663,13 +663,21 @@ void bwd_dkdv_wide_kernel(const BwdParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31, hh = lane >> 5;
+  // Workgroup = (pair rank, split s), as in bwd_dkdv_kernel: split s of
+  // dkv_split takes an equal share of the pair's row blocks in the loop's
+  // order (all of them without a split) and leaves fp32 partials.
+  const int split = p.dkv_split;
+  const int pair = blockIdx.x / split;
+  const int s_idx = blockIdx.x - pair * split;
   int t, kvh;
-  dkv_pair(p, blockIdx.x, t, kvh);
+  dkv_pair(p, pair, t, kvh);
   const int nt = p.kv_tiles_dkv;
   const int b0lo = p.ranges[2 * t], b0hi = p.ranges[2 * t + 1];
   const int b1lo = p.ranges[2 * (nt + t)], b1hi = p.ranges[2 * (nt + t) + 1];
   const int n0 = max(b0hi - b0lo, 0), n1 = max(b1hi - b1lo, 0);
-  const int nb = n0 + n1;
+  const int chunk = (n0 + n1 + split - 1) / split;
+  const int first = min(n0 + n1, s_idx * chunk);
+  const int nb = min(n0 + n1 - first, chunk);
   const int pb0 = static_cast<int>(packed_block(p, 0, kvh, b0lo));
   const int pb1 = static_cast<int>(packed_block(p, 1, kvh, b1lo)) - n0;
   const int kw0 = t * kKeysDkv + 64 * wave;
@@ -736,6 +744,11 @@ void bwd_dkdv_wide_kernel(const BwdParams p) {
   const uint32_t vb_hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(vbase >> 32));
   const uint64_t vb64 = (static_cast<uint64_t>(vb_hi) << 32) | vb_lo;
   const float c = p.c, scale = p.scale;
+  // This wave's split partials: the reduce's waves 2 wave and 2 wave + 1.
+  const char* part = split > 1 ? reinterpret_cast<const char*>(p.dkv_part) +
+                                     (static_cast<int64_t>(blockIdx.x) * kBwdWaves + 2 * wave) * kPartUnits * 1024
+                               : reinterpret_cast<const char*>(p.dk);
+  const i32x4 prsrc = make_rsrc(part, split > 1 ? 2 * kPartUnits * 1024 : 0);
   asm volatile(SWATTN_BWD_DKDV_ASM
                :
                : [qrsrc] "s"(qrsrc), [dorsrc] "s"(dorsrc), [irsrc] "s"(irsrc), [krsrc] "s"(krsrc),
@@ -743,8 +756,9 @@ void bwd_dkdv_wide_kernel(const BwdParams p) {
                  [vbytes] "s"(__builtin_amdgcn_readfirstlane(vbytes)),
                  [nblk] "s"(__builtin_amdgcn_readfirstlane(nb)),
                  [pb1n] "s"(__builtin_amdgcn_readfirstlane(pb1 + n0)),
-                 [pbf] "s"(__builtin_amdgcn_readfirstlane(pb0 + n0 - 1)),
-                 [pb1] "s"(__builtin_amdgcn_readfirstlane(pb1)),
+                 [pbf] "s"(__builtin_amdgcn_readfirstlane(pb0 + n0 - 1 - first)),
+                 [pb1] "s"(__builtin_amdgcn_readfirstlane(pb1 + first)),
+                 [prsrc] "s"(prsrc), [split] "s"(__builtin_amdgcn_readfirstlane(split > 1 ? 1 : 0)),
                  [kw0] "s"(__builtin_amdgcn_readfirstlane(kw0)),
                  [krow4] "s"(__builtin_amdgcn_readfirstlane(static_cast<int>(4 * krowbytes))),
                  [vl] "s"(__builtin_amdgcn_readfirstlane(lds0 + 64 * wave * kRowBytes)),
@@ -1315,18 +1329,17 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // comparisons.
 // bwd_dkdv_wide_kernel gathers rows by 32-bit offsets into Q / dO and reads
 // K, V, dK, dV and the row info through 32-bit buffer ranges (all below
-// 2^31 bytes).  It runs where the pairs need no split;
-// SWATTN_DKDV_KERNEL=narrow picks the eight-wave kernel everywhere, =wide
-// the 64-key kernel also where the eight-wave one would split (tests).
+// 2^31 bytes).  It runs split or unsplit, as the layout decides;
+// SWATTN_DKDV_KERNEL=narrow picks the eight-wave kernel (tests and
+// comparisons).
 inline bool use_dkdv_wide(int64_t total_q, int64_t total_kv, int32_t heads_q, int32_t heads_kv,
-                          int64_t total_blocks, int64_t split) {
+                          int64_t total_blocks) {
   if (total_q * heads_q * kRowBytes >= (int64_t{1} << 31)) return false;
   if (total_kv * heads_kv * kRowBytes >= (int64_t{1} << 31)) return false;
   if (total_blocks * kInfoBytes >= (int64_t{1} << 31)) return false;
   const char* force = getenv("SWATTN_DKDV_KERNEL");
   if (force != nullptr && strcmp(force, "narrow") == 0) return false;
-  if (force != nullptr && strcmp(force, "wide") == 0) return true;
-  return split == 1;
+  return true;
 }
 
 inline bool use_dq_wide(int64_t total_q, int64_t total_kv, int32_t heads_q, int32_t heads_kv) {
@@ -1540,16 +1553,14 @@ extern "C" int swattn_prefill_bwd(const void* q, const void* k, const void* v, c
                          dim3(kThreads), 0, st, p);
   }
   const int64_t pairs = L.kv_tiles_dkv * heads_kv;
-  const bool dkdv_wide = use_dkdv_wide(total_q, total_kv, heads_q, heads_kv, L.total_blocks, L.dkv_split);
-  if (dkdv_wide) {
-    BwdParams pw = p;
-    pw.dkv_split = 1;   // every pair whole: no partials
-    hipLaunchKernelGGL(bwd_dkdv_wide_kernel, dim3(static_cast<uint32_t>(pairs)), dim3(256), 0, st, pw);
-  } else {
+  const bool dkdv_wide = use_dkdv_wide(total_q, total_kv, heads_q, heads_kv, L.total_blocks);
+  if (dkdv_wide)
+    hipLaunchKernelGGL(bwd_dkdv_wide_kernel, dim3(static_cast<uint32_t>(pairs * L.dkv_split)), dim3(256), 0,
+                       st, p);
+  else
     hipLaunchKernelGGL(bwd_dkdv_kernel, dim3(static_cast<uint32_t>(pairs * L.dkv_split)),
                        dim3(kBwdThreads), 0, st, p);
-  }
-  if (!dkdv_wide && L.dkv_split > 1)
+  if (L.dkv_split > 1)
     hipLaunchKernelGGL(bwd_dkdv_reduce_kernel,
                        dim3(static_cast<uint32_t>(pairs * kBwdWaves * kPartUnits * 64 / kThreads)),
                        dim3(kThreads), 0, st, p);

@@ -1,11 +1,13 @@
 """The backward's 64-key-per-wave dK/dV kernel (bwd_dkdv_wide_kernel)
 against the oracle and against the eight-wave dK/dV kernel.
 
-The 64-key kernel is the default where the eight-wave kernel would not
-split its (key tile, KV head) pairs (512 pairs or more); SWATTN_DKDV_KERNEL
-=wide forces it (unsplit) on the small shapes of test_gpu_backward, =narrow
-forces the eight-wave kernel.  Where neither splits, their dq is the same
-kernel's and agrees bit for bit.  Their dk and dv differ in rounding only:
+The 64-key kernel is the default; under 512 (key tile, KV head) pairs it
+shares each pair's row blocks out over several workgroups whose fp32
+partials the reduce kernel adds, as the eight-wave kernel does.
+SWATTN_DKDV_KERNEL=wide names it explicitly on the small shapes below (all
+split), =narrow forces the eight-wave kernel.  Both take the same split and
+the same dQ kernel, so dq agrees bit for bit.  Their dk and dv differ in
+rounding only:
 the 64-key kernel takes a pair's full-branch row blocks from the last down
 (the eight-wave kernel from the first up), so the fp32 sums run in another
 order, and it takes dP - Delta from the matrix cores (the accumulation
@@ -96,11 +98,14 @@ def test_wide_dkdv_varlen_metadata(monkeypatch):
 @pytest.mark.parametrize("b,s,hq,hkv,w,p", [
     (1, 8192, 16, 16, 512, 0.3),     # 32 key tiles x 16 KV heads = 512 pairs: no split
     (2, 4096, 32, 16, 300, 0.5),     # two sequences, 512 pairs
+    (2, 4096, 32, 8, 1024, 0.25),    # 256 pairs: split in two
+    (1, 16384, 4, 1, 1024, 0.25),    # one KV head, 64 pairs: split in eight
+    (1, 1024, 8, 2, 256, 0.25),      # 8 pairs: the largest split
 ])
-def test_wide_dkdv_matches_eight_wave_where_unsplit(monkeypatch, b, s, hq, hkv, w, p):
-    """Where the eight-wave kernel does not split, the default (64-key)
-    kernel's dk and dv match it within the bar above (dq bit for bit), and
-    reruns are bit-identical."""
+def test_wide_dkdv_matches_eight_wave(monkeypatch, b, s, hq, hkv, w, p):
+    """The default (64-key) kernel's dk and dv match the eight-wave
+    kernel's within the bar above (dq bit for bit), split or not, and reruns
+    are bit-identical."""
     q, k, v, do = _qkv(b * 7 + s, b, s, hq, hkv)
     m = _mask(s + 9, (b, s), p)
     wide = _run(q, k, v, do, m, w)
