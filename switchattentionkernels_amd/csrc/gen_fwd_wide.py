@@ -106,6 +106,8 @@ V_MK = 206                           # 206..209 mask temporaries
 V_LO = 210                           # [rb] mask: row start - 4 hh - first key of the tile
 V_T = 188                            # epilogue temporaries (the loop's registers are free by then)
 V_EPI = 209                          # 209..215 epilogue lane addresses
+V_THR = 212                          # the row-sum check's threshold (loop only)
+V_CHK = 213                          # row-sum check temporary (loop only)
 V_LIMIT = 216                        # first VGPR left to the compiler
 
 # clobbered SGPRs
@@ -117,15 +119,18 @@ S_N = 65                    # tile count
 S_SPAN = 66                 # it1 - it0: tiles r + 1 - it0 below it need no range mask
 S_KEY0 = 67                 # first key of tile r + 1 (masked steps)
 S_KBYTES, S_VBYTES = 68, 69  # bytes from the current K / V^T descriptor base to the item's end
+S_FORCE = 70                # nonzero: the next tile's half-0 check fails (2)
+S_FORCE1 = 90               # nonzero: this tile's half-1 check fails (2)
 S_KRS, S_VRS = 72, 76       # K / V^T buffer descriptors (4 each)
 S_PAIRS = (80, 82, 84, 86)  # VALU compare results (2 each)
 S_EIGHT, S_SENT = 88, 89    # 8.0 and the -2^30 max sentinel
-S_FIRST, S_LASTC = 52, 89   # clobbered range
+S_FIRST, S_LASTC = 52, 91   # clobbered range
 
 SENTINEL_BITS = 0xCE800000   # -2^30 as fp32 (V:174)
 NEG_INF_BITS = 0xFF800000
 EIGHT_BITS = 0x41000000
 RSRC_WORD3 = 0x00020000
+THR_BITS = 0x46000000        # 8192.0: a half passes its check when every lane's 16-key sum is at most this
 
 TILE_BYTES = 16384           # one K or V^T tile in LDS
 K_SLOTS = V_SLOTS = 4        # tile j+1's K and tile j's V^T are staged three steps before step j
@@ -300,11 +305,13 @@ def half_elems(s, h):
     return out
 
 
-def exps(s, h, lo, hi):
-    """P = 2^(s c - m c) in place for elements lo..hi-1 of half h."""
+def exps(s, h, lo, hi, nh=None):
+    """P = 2^(s c + n) in place for elements lo..hi-1 of half h, with n the
+    running -m c after half nh (default h) of the last tile whose max was
+    taken."""
     out = []
     for rb, x in half_elems(s, h)[lo:hi]:
-        nmc = V_NMC + 2 * h + rb
+        nmc = V_NMC + 2 * (h if nh is None else nh) + rb
         out.append(valu(f"v_fma_f32 {vreg(x)}, {vreg(x)}, {s_in('c')}, {vreg(nmc)}",
                         {f"v{x}", f"v{nmc}"}, {f"v{x}"}))
         out[-1].feeds_trans = True
@@ -337,6 +344,12 @@ def sums(s, h):
     """Row sums of the fp32 P of half h (in place, after its packing), added
     to this lane's partial l (the two lanes of a row keep partial sums of
     their own keys; they are combined once, at the end)."""
+    return sums_tree(s, h) + sums_add(s, h)
+
+
+def sums_tree(s, h):
+    """This lane's sum of its 16 fp32 P of half h for each row block, in
+    place (after the packing), left in the half's first register."""
     out = []
     width = 16
     while width > 1:
@@ -347,6 +360,12 @@ def sums(s, h):
                 out.append(valu(f"v_add_f32 {vreg(b + i)}, {vreg(b + i)}, {vreg(b + i + hw)}",
                                 {f"v{b + i}", f"v{b + i + hw}"}, {f"v{b + i}"}))
         width = hw
+    return out
+
+
+def sums_add(s, h):
+    """The half's lane sums (sums_tree) added to this lane's partial l."""
+    out = []
     for rb in range(2):
         b = s + 32 * rb + 16 * h
         out.append(valu(f"v_add_f32 {vreg(V_L + rb)}, {vreg(V_L + rb)}, {vreg(b)}",
@@ -411,15 +430,16 @@ def running_max(s, h, par):
     return out
 
 
-def mask(s, h):
+def mask(s, h, key0=S_KEY0):
     """Scores of half h outside each row's [start, end) set to -inf.
     Register r of the half is key 32 h + 8 (r >> 2) + 4 hh + (r & 3) of the
     tile; the row bounds were shifted by 4 hh, so it is legal iff
-    (off - lo) < span, unsigned, with lo = start - 4 hh - key0."""
+    (off - lo) < span, unsigned, with lo = start - 4 hh - key0 (the tile's
+    first key, in SGPR key0)."""
     out = []
     for rb in range(2):
-        out.append(valu(f"v_subrev_u32 {vreg(V_LO + rb)}, {sreg(S_KEY0)}, {vreg(V_KSR + rb)}",
-                        {f"v{V_KSR + rb}", f"s{S_KEY0}"}, {f"v{V_LO + rb}"}))
+        out.append(valu(f"v_subrev_u32 {vreg(V_LO + rb)}, {sreg(key0)}, {vreg(V_KSR + rb)}",
+                        {f"v{V_KSR + rb}", f"s{key0}"}, {f"v{V_LO + rb}"}))
     elems = [(rb, r) for rb in range(2) for r in range(16)]
     for g in range(0, len(elems), 4):
         grp = elems[g:g + 4]
@@ -644,11 +664,39 @@ def schedule(mfmas, valu_list, side=None, carry=False, n_carried=0, lead_cap=2, 
 # (read by step r-1) and V^T(r+3) into V^T slot (q+3)%4 (read by step r-1),
 # and at its end reads the first operands of K(r+2) and V^T(r+1).
 
-def block_a(q, kind, masked):
+def split_left(left, regs_):
+    """Leftover work of a block before a check: what touches regs_ (or must
+    precede such work) is issued at the block's end, the rest is carried
+    on.  Both lists keep their program order."""
+    must = [bool((x.rd | x.wr | x.mask_rd) & regs_) for x in left]
+    for j in reversed(range(len(left))):
+        if must[j]:
+            for i in range(j):
+                if not must[i] and _conflict(left[i], left[j]):
+                    must[i] = True
+    return [x for x, m in zip(left, must) if m], [x for x, m in zip(left, must) if not m]
+
+
+def half_regs(s, h):
+    """The S / P registers of half h of the tile at s, and its P^T operands."""
+    r = {f"v{s + 32 * rb + 16 * h + i}" for rb in range(2) for i in range(16)}
+    return r | regs("v", PK_V + 16 * h, 16)
+
+
+# the temporaries of mask() and the row sums a recomputation also writes
+CHECK_TEMPS = ({f"v{V_L}", f"v{V_L + 1}", f"v{V_CHK}"} | regs("v", V_LO, 2) | regs("v", V_MK, 4) |
+               regs("s", S_PAIRS[0], 8) | regs("s", S_T0, 2))
+
+
+def block_a(q, kind, masked, opt=False):
     """S(j+1) = K(j+1) Q^T in 32 MFMAs (half 0, then half 1) while P(j)
     half 1 is exponentiated, P(j) half 0 packed and summed, and S(j+1)
     half 0's running max taken.  kind 'pre' (tile 0's S only), 'full',
-    'last' (no S(j+1)).  Returns (instructions, leftover VALU)."""
+    'last' (no S(j+1)).  With opt no running max is taken, P(j) half 0's
+    lane sums stay for its check, and P(j) half 1 is also packed and its
+    lane sums formed; what is left over of that half 1 work is carried on
+    (the rest is issued before the check).  Returns (instructions,
+    leftover VALU)."""
     par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
     pn = 1 - par           # parity of tile j + 1
@@ -656,13 +704,18 @@ def block_a(q, kind, masked):
     out = []
     vl = []
     if kind != "pre":
-        vl += exps(scur, 1, 0, 32) + packs(scur, 0) + sums(scur, 0)
+        vl += exps(scur, 1, 0, 32) + packs(scur, 0) + (sums_tree(scur, 0) if opt else sums(scur, 0))
+        if opt:
+            vl += check_items(par, 0)
     if kind != "last":
         if masked:
             out += [salu(f"s_lshl_b32 {sreg(S_KEY0)}, {sreg(S_R1)}, 6"),
                     salu(f"s_add_u32 {sreg(S_KEY0)}, {sreg(S_KEY0)}, {s_in('key0')}")]
             vl += mask(snxt, 0)
-        vl += running_max(snxt, 0, pn)
+        if not opt:
+            vl += running_max(snxt, 0, pn)
+    if opt and kind != "pre":
+        vl += packs(scur, 1) + sums_tree(scur, 1)
     if kind == "last":
         out += [v_read(*x, q) for x in V_SEQ[N_PRE_V:V_SETS - 1]]
         o, _ = schedule([], vl)
@@ -691,26 +744,36 @@ def block_a(q, kind, masked):
             r.append(v_read(*vre[(i - 26) // 2], q))
         return r
     o, left = schedule(mf, vl, side, carry=True)
+    if opt:
+        must, left = split_left(left, half_regs(scur, 0) | CHECK_TEMPS)
+        o += must
     return out + o, left
 
 
-def block_b1(q, kind, masked, carried):
+def block_b1(q, kind, masked, carried, opt=False):
     """P(j) V(j) for half 0 (16 MFMAs) while S(j+1) half 0 is exponentiated
     (first 16 of 32), P(j) half 1 packed and S(j+1) half 1's running max
-    taken.  Returns (instructions, leftover VALU)."""
+    taken.  With opt: P(j) half 0's lane sums are added to l first, S(j+1)
+    half 0 is exponentiated with the running max as it stands, no max is
+    taken, and what is left over of P(j) half 1 or the masks is issued
+    before the half-1 check (the exponentials are carried on).  Returns
+    (instructions, leftover VALU)."""
     par = q % 2
     snxt, scur = S_V[1 - par], S_V[par]
     pn = 1 - par
     vl = list(carried)
     nc = len(vl)
+    if opt and kind != "pre":
+        vl += check_items(par, 1) + sums_add(scur, 0)
     if kind != "last":
-        vl += exps(snxt, 0, 0, 16)
-    if kind != "pre":
+        vl += exps(snxt, 0, 0, 16, nh=1 if opt else None)
+    if kind != "pre" and not opt:
         vl += packs(scur, 1)
     if kind != "last":
         if masked:
             vl += mask(snxt, 1)
-        vl += running_max(snxt, 1, pn)
+        if not opt:
+            vl += running_max(snxt, 1, pn)
     dmas = [dma("v", i, (q + 3) % 4) for i in range(4)] if kind != "last" else []
     if kind == "pre":
         o, _ = schedule([], vl)
@@ -733,22 +796,28 @@ def block_b1(q, kind, masked, carried):
                 r += desc_advance("v")
         return r
     o, left = schedule(mf, vl, side, carry=True, n_carried=nc, lead_cap=0)
+    if opt:
+        must, left = split_left(left, half_regs(scur, 1) | CHECK_TEMPS)
+        o += must
     for x in left:
         assert f"v{V_L}" not in x.wr, "the half-0 row sums must be added before the half-1 rescale"
     return o, left
 
 
-def block_b2(q, kind, carried):
+def block_b2(q, kind, carried, opt=False):
     """P(j) V(j) for half 1 (16 MFMAs) while S(j+1) half 0's last 16
-    exponentials run and P(j) half 1 is summed; then the next step's first
-    K(j+2) and V^T(j+1) operands are read."""
+    exponentials run and P(j) half 1 is summed (with opt: its lane sums,
+    formed before the check, added to l); then the next step's first K(j+2)
+    and V^T(j+1) operands are read."""
     par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
     vl = list(carried)
     nc = len(vl)
+    if opt and kind != "pre":
+        vl += sums_add(scur, 1)
     if kind != "last":
-        vl += exps(snxt, 0, 16, 32)
-    if kind != "pre":
+        vl += exps(snxt, 0, 16, 32, nh=1 if opt else None)
+    if kind != "pre" and not opt:
         vl += sums(scur, 1)
     mf = []
     if kind != "pre":
@@ -774,8 +843,6 @@ def block_b2(q, kind, carried):
 
 
 # ---------------------------------------------------------------------------
-# program
-# ---------------------------------------------------------------------------
 
 
 class Block:
@@ -785,35 +852,185 @@ class Block:
         self.ret_point = ret_point    # the rescale routine may return here
 
 
-def call_rescale(tag, par, h):
-    """Blocks that apply O, l *= 2^-e(tile of parity par, half h) when that
-    tile half's flag is set: test, then (rarely) give each row block its
-    exponents, drain the LDS reads and branch to the shared routine with
-    the return address."""
+COLD = []     # out-of-line call blocks, laid out after the loop
+
+
+def _cold_call(tag, skip, target, prep=()):
+    """An out-of-line block that drains the LDS reads, sets the return
+    address to `skip` and branches to the routine at `target`.  The block
+    is laid out after `skip` (program() places COLD after every step), so
+    the return address is the program counter minus a positive distance
+    (a 64-bit subtraction: adding the negative 32-bit difference with a
+    carry into the high word would be off by 2^32); generate() checks the
+    order."""
     u = "%="
-    flag = S_FLAG + 4 * par + 2 * h
-    skip, pc = f"L{tag}_x_{u}", f"L{tag}_pc_{u}"
-    al = V_AL + 2 * par + h
-    test = Block(f"L{tag}_t_{u}", [salu(f"s_cmp_lg_u64 {sreg(flag, 2)}, 0"), branch("s_cbranch_scc0", skip)])
-    call = Block(f"L{tag}_c_{u}", [
-        valu(f"v_mov_b32 {vreg(V_RA)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA}"}),
-        valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA + 1}"}),
-        Ins(f"v_permlane32_swap_b32 {vreg(V_RA)}, {vreg(V_RA + 1)}", "perm", {f"v{V_RA}", f"v{V_RA + 1}"},
-            {f"v{V_RA}", f"v{V_RA + 1}"}),
+    pc = f"L{tag}_pc_{u}"
+    COLD.append(Block(f"L{tag}_c_{u}", list(prep) + [
         waitcnt(lgkm=0),
         Ins(f"s_getpc_b64 {sreg(S_RET, 2)}", "salu", set(), {f"s{S_RET}", f"s{S_RET + 1}"}),
         label(pc),
-        salu(f"s_add_u32 {sreg(S_RET)}, {sreg(S_RET)}, {skip}-{pc}"),
-        salu(f"s_addc_u32 {sreg(S_RET + 1)}, {sreg(S_RET + 1)}, 0"),
-        Ins(f"s_branch Lrescale_{u}", "call", branch=f"Lrescale_{u}", cond=False),
-    ])
-    return [test, call, Block(skip, [], ret_point=True)]
+        salu(f"s_sub_u32 {sreg(S_RET)}, {sreg(S_RET)}, {pc}-{skip}"),
+        salu(f"s_subb_u32 {sreg(S_RET + 1)}, {sreg(S_RET + 1)}, 0"),
+        Ins(f"s_branch {target}", "call", branch=target, cond=False),
+    ]))
+    return f"L{tag}_c_{u}"
 
 
-def step_blocks(tag, q, kind, end_label):
+def check_returns(blocks):
+    """Every return address is formed as pc - (pc - skip): the skip label
+    must come before the call's pc label in the layout."""
+    pos = {}
+    n = 0
+    for b in blocks:
+        pos[b.name] = n
+        for ins in b.ins:
+            n += 1
+            if ins.kind == "label":
+                pos[ins.text[:-1]] = n
+    for b in blocks:
+        for ins in b.ins:
+            if ins.text.startswith(f"s_sub_u32 {sreg(S_RET)}, {sreg(S_RET)}, "):
+                pc, skip = ins.text.split(", ")[-1].split("-")
+                assert pos[skip] < pos[pc], f"return label {skip} after its call"
+            assert not ins.text.startswith(f"s_add_u32 {sreg(S_RET)},"), "return address formed by an add"
+
+
+def call_rescale(tag, par, h):
+    """Blocks that apply O, l *= 2^-e(tile of parity par, half h) when that
+    tile half's flag is set: test (and clear) the flag, then (rarely, out
+    of line) give each row block its exponents, drain the LDS reads and
+    branch to the shared routine with the return address."""
+    u = "%="
+    flag = S_FLAG + 4 * par + 2 * h
+    skip = f"L{tag}_x_{u}"
+    al = V_AL + 2 * par + h
+    call = _cold_call(tag, skip, f"Lrescale_{u}", [
+        valu(f"v_mov_b32 {vreg(V_RA)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA}"}),
+        valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA + 1}"}),
+        Ins(f"v_permlane32_swap_b32 {vreg(V_RA)}, {vreg(V_RA + 1)}", "perm", {f"v{V_RA}", f"v{V_RA + 1}"},
+            {f"v{V_RA}", f"v{V_RA + 1}"})])
+    # the flag is cleared once tested: steps that take no running max leave
+    # it clear unless a recomputation sets it
+    test = Block(f"L{tag}_t_{u}", [salu(f"s_cmp_lg_u64 {sreg(flag, 2)}, 0"),
+                                   salu(f"s_mov_b64 {sreg(flag, 2)}, 0", wr={f"s{flag}", f"s{flag + 1}"}),
+                                   branch("s_cbranch_scc1", call)])
+    return [test, Block(skip, [], ret_point=True)]
+
+
+def call_recompute(tag, par, h, head):
+    """Blocks that end `head` with the check of half h of tile j (parity
+    par): every lane's 16-key sums of its two row blocks (left by
+    sums_tree) at most the threshold, and no recomputation forced;
+    else (rarely, out of line) drain the LDS reads and branch to the shared
+    routine that recomputes the half's scores with the exact running max."""
+    u = "%="
+    skip = f"L{tag}_x_{u}"
+    pr = S_T0
+    call = _cold_call(tag, skip, f"Lrecomp{par}{h}_{u}")
+    chk = [salu(f"s_cmp_lg_u64 {sreg(pr, 2)}, 0", {f"s{pr}", f"s{pr + 1}"}), branch("s_cbranch_scc1", call)]
+    return [Block(f"L{tag}_k_{u}", head + chk), Block(skip, [], ret_point=True)]
+
+
+def check_items(par, h):
+    """The test of half h of tile j (parity par) that call_recompute
+    branches on, as ordinary work for the scheduler: s[S_T0:S_T0+1] = lanes
+    whose 16-key sum of either row block (left by sums_tree) exceeds the
+    threshold, or every lane when a recomputation is forced."""
+    s = S_V[par]
+    pr = S_T0
+    force = S_FORCE if h == 0 else S_FORCE1
+    return [valu(f"v_max_f32 {vreg(V_CHK)}, {vreg(s + 16 * h)}, {vreg(s + 32 + 16 * h)}",
+                 {f"v{s + 16 * h}", f"v{s + 32 + 16 * h}"}, {f"v{V_CHK}"}),
+            valu(f"v_cmp_lt_f32_e64 {sreg(pr, 2)}, {vreg(V_THR)}, {vreg(V_CHK)}", {f"v{V_THR}", f"v{V_CHK}"},
+                 {f"s{pr}", f"s{pr + 1}"}),
+            # mask_rd: keeps the scalar read three instructions after the compare
+            Ins(f"s_or_b64 {sreg(pr, 2)}, {sreg(pr, 2)}, {sreg(force, 2)}", "salu",
+                {f"s{force}", f"s{force + 1}"}, {f"s{pr}", f"s{pr + 1}"}, mask_rd={f"s{pr}", f"s{pr + 1}"})]
+
+
+def recompute_routine(par, h):
+    """Half h of tile j = r of step r (S_R1 - 1; scores in S buffer par)
+    failed its check: its exponentials may exceed the threshold or be
+    infinite, or (half 1) the max moved in half 0 after they were taken.
+    Its K rows come straight from memory (the LDS slot is being refilled);
+    the half's scores are recomputed by the same MFMAs in the same order,
+    masked, given the exact running max (O, l *= 2^-e then follows at the
+    step's rescale point), exponentiated, packed and summed as the step
+    would have.  Where a row's max moved from a finite value, the
+    exponentials taken since with the old max are redone too: half 0 forces
+    half 1's check, half 1 the next tile's half-0 check.  Entered by a
+    branch with the return address in S_RET."""
+    s = S_V[par]
+    rs, t0, t1 = S_PAIRS[2], S_T0, S_T1
+    o0, lane = V_RS, s_in("lane")
+    out = [salu(f"s_sub_u32 {sreg(t0)}, {sreg(S_R1)}, 1", {f"s{S_R1}"}, {f"s{t0}"}),
+           salu(f"s_mul_i32 {sreg(t0)}, {sreg(t0)}, {s_in('ktilebytes')}", {f"s{t0}"}, {f"s{t0}"}),
+           salu(f"s_mov_b64 {sreg(rs, 2)}, {s_in('kbase')}", set(), {f"s{rs}", f"s{rs + 1}"}),
+           salu(f"s_add_u32 {sreg(rs)}, {sreg(rs)}, {sreg(t0)}", {f"s{rs}", f"s{t0}"}, {f"s{rs}"}),
+           salu(f"s_addc_u32 {sreg(rs + 1)}, {sreg(rs + 1)}, 0", {f"s{rs + 1}"}, {f"s{rs + 1}"}),
+           salu(f"s_sub_i32 {sreg(rs + 2)}, {s_in('kbytes')}, {sreg(t0)}", {f"s{t0}"}, {f"s{rs + 2}"}),
+           salu(f"s_max_i32 {sreg(rs + 2)}, {sreg(rs + 2)}, 0", {f"s{rs + 2}"}, {f"s{rs + 2}"}),
+           salu(f"s_mov_b32 {sreg(rs + 3)}, {RSRC_WORD3:#x}", set(), {f"s{rs + 3}"}),
+           salu(f"s_lshr_b32 {sreg(t1)}, {s_in('ktilebytes')}, 6", set(), {f"s{t1}"}),
+           # lane l loads key 32 h + (l & 31), head_dim 8 (l >> 5) + 16 kk
+           valu(f"v_and_b32 {vreg(o0)}, 31, {lane}", set(), {f"v{o0}"}),
+           valu(f"v_add_u32 {vreg(o0)}, {32 * h}, {vreg(o0)}", {f"v{o0}"}, {f"v{o0}"}),
+           valu(f"v_mul_u32_u24 {vreg(o0)}, {sreg(t1)}, {vreg(o0)}", {f"v{o0}", f"s{t1}"}, {f"v{o0}"}),
+           valu(f"v_lshrrev_b32 {vreg(o0 + 1)}, 5, {lane}", set(), {f"v{o0 + 1}"}),
+           valu(f"v_lshl_add_u32 {vreg(o0)}, {vreg(o0 + 1)}, 4, {vreg(o0)}", {f"v{o0}", f"v{o0 + 1}"},
+                {f"v{o0}"})]
+    for kk in range(8):
+        d = KOP_A + 4 * kk
+        out.append(Ins(f"buffer_load_dwordx4 {areg(d, 4)}, {vreg(o0)}, {sreg(rs, 4)}, 0 offen offset:{32 * kk}",
+                       "vmem_ld", {f"v{o0}"} | regs("s", rs, 4), regs("a", d, 4), vm=True))
+    out.append(waitcnt(vm=0))
+    for kk in range(8):
+        for rb in range(2):
+            out.append(mfma(("v", s + 32 * rb + 16 * h), ("a", KOP_A + 4 * kk), ("a", Q_A + 8 * kk + 4 * rb),
+                            kk > 0))
+    out += [salu(f"s_sub_u32 {sreg(t0)}, {sreg(S_R1)}, 1", {f"s{S_R1}"}, {f"s{t0}"}),
+            salu(f"s_lshl_b32 {sreg(t0)}, {sreg(t0)}, 6", {f"s{t0}"}, {f"s{t0}"}),
+            salu(f"s_add_u32 {sreg(t0)}, {sreg(t0)}, {s_in('key0')}", {f"s{t0}"}, {f"s{t0}"})]
+    vl = mask(s, h, key0=t0) + running_max(s, h, par) + exps(s, h, 0, 32) + packs(s, h) + sums_tree(s, h)
+    if h == 0:
+        # the steps without a running max exponentiate with n after half 1
+        vl += [valu(f"v_mov_b32 {vreg(V_NMC + 2 + rb)}, {vreg(V_NMC + rb)}", {f"v{V_NMC + rb}"},
+                    {f"v{V_NMC + 2 + rb}"}) for rb in range(2)]
+    o, _ = schedule([], vl)
+    out += o
+    flag = S_FLAG + 4 * par + 2 * h
+    fset, fclr = (S_FORCE1, S_FORCE) if h == 0 else (S_FORCE, S_FORCE1)
+    out += [salu(f"s_mov_b64 {sreg(fset, 2)}, {sreg(flag, 2)}", {f"s{flag}", f"s{flag + 1}"},
+                 {f"s{fset}", f"s{fset + 1}"}),
+            salu(f"s_mov_b64 {sreg(fclr, 2)}, 0", set(), {f"s{fclr}", f"s{fclr + 1}"}),
+            Ins("s_nop 15", "nop"),
+            Ins(f"s_setpc_b64 {sreg(S_RET, 2)}", "ret")]
+    return out
+
+
+def opt_tail(tag, q, kind, masked):
+    """A step without running max: its A block and the check of P(j) half
+    0, O, l *= 2^-e(j, 0) if needed, B1 and the check of P(j) half 1, O, l
+    *= 2^-e(j, 1) if needed, B2 (work left over by one block carried into
+    the next)."""
+    u = "%="
+    par = q % 2
+    a, left = block_a(q, kind, masked, opt=True)
+    bl = call_recompute(f"{tag}k0", par, 0, a)
+    bl += call_rescale(f"{tag}r0", par, 0)
+    b1, left = block_b1(q, kind, masked, left, opt=True)
+    bl += call_recompute(f"{tag}k1", par, 1, b1)
+    bl += call_rescale(f"{tag}r1", par, 1)
+    bl.append(Block(f"L{tag}_b2_{u}", block_b2(q, kind, left, opt=True)))
+    return bl
+
+
+def step_blocks(tag, q, kind, end_label, opt=True):
     """kind: 'pre' (S of the first tile only), 'full', 'last' (P V only).
-    A full step: wait and barrier, O, l *= 2^-e(j, 0) if needed, then an
-    unmasked or a masked copy of A, B1, O, l *= 2^-e(j, 1) if needed, B2."""
+    A full step with the running max (opt False): wait and barrier, O, l *=
+    2^-e(j, 0) if needed, then an unmasked or a masked copy of A, B1, O, l
+    *= 2^-e(j, 1) if needed, B2.  Without it (opt): wait and barrier, then
+    an unmasked or a masked copy of A and opt_tail."""
     u = "%="
     par = q % 2
     blocks = []
@@ -829,6 +1046,23 @@ def step_blocks(tag, q, kind, end_label):
     # 8 of the previous step may still be in flight, and so may the operand
     # reads that step issued last (from slots no DMA of this step writes).
     blocks.append(Block(f"L{tag}_s_{u}", [waitcnt(vm=8, lgkm=N_PRE_K + N_PRE_V), Ins("s_barrier", "barrier")]))
+    if opt:
+        if kind == "last":
+            blocks += opt_tail(f"{tag}L", q, "last", False)
+            blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
+            return blocks
+        blocks.append(Block(f"L{tag}_mt_{u}", [salu(f"s_sub_u32 {sreg(S_T1)}, {sreg(S_R1)}, {s_in('it0')}"),
+                                               salu(f"s_cmp_ge_u32 {sreg(S_T1)}, {sreg(S_SPAN)}"),
+                                               branch("s_cbranch_scc1", f"L{tag}_am_{u}")]))
+        for masked in (False, True):
+            mt = "m" if masked else "u"
+            bl = opt_tail(f"{tag}{mt}", q, kind, masked)
+            bl[0].name = f"L{tag}_a{mt}_{u}"
+            blocks += bl
+            if not masked:
+                blocks.append(Block(f"L{tag}_j_{u}", [branch("s_branch", end_label, cond=False)]))
+        return blocks
+    assert kind == "full"
     blocks += call_rescale(f"{tag}r0", par, 0)
     if kind == "last":
         a, left = block_a(q, "last", False)
@@ -923,6 +1157,9 @@ def prologue():
     for k in range(4):
         out.append(valu(f"v_mov_b32 {vreg(V_NMC + k)}, {vreg(V_NSENT)}", {f"v{V_NSENT}"}, {f"v{V_NMC + k}"}))
     out.append(valu(f"v_mov_b32 {vreg(V_NINF)}, {NEG_INF_BITS:#x}", set(), {f"v{V_NINF}"}))
+    out.append(valu(f"v_mov_b32 {vreg(V_THR)}, {THR_BITS:#x}", set(), {f"v{V_THR}"}))
+    for f in (S_FORCE, S_FORCE1):
+        out.append(salu(f"s_mov_b64 {sreg(f, 2)}, 0", set(), {f"s{f}", f"s{f + 1}"}))
     # Q and K(0) have landed in every wave (K(1), V^T(0), K(2), V^T(1) may
     # still be in flight: 16 DMAs)
     out += [waitcnt(vm=PRO_LATE), Ins("s_barrier", "barrier")]
@@ -1011,20 +1248,34 @@ def program():
                                                   branch("s_cbranch_scc1", f"Lepi_{u}")])]
     blocks += step_blocks("p", 3, "pre", None)
     blocks.append(Block(f"Lr0_{u}", [salu(f"s_mov_b32 {sreg(S_R1)}, 1")]))
-    for q in range(4):
+    # Step 0 takes the exact running max of tile 1 (as the pre step does of
+    # tile 0), so that every row whose range starts within the first two
+    # tiles has a finite max before the steps without one; it is phase 0.
+    blocks.append(Block(f"Le_{u}", [salu(f"s_cmp_ge_i32 {sreg(S_R1)}, {sreg(S_N)}"),
+                                    branch("s_cbranch_scc1", f"Llast0_{u}")]))
+    blocks += step_blocks("e", 0, "full", f"Leinc_{u}", opt=False)
+    blocks.append(Block(f"Leinc_{u}", [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")]))
+    # the loop, laid out from phase 1 (step 0 falls into it there)
+    for q in (1, 2, 3, 0):
         blocks.append(Block(f"Lt{q}_{u}", [salu(f"s_cmp_ge_i32 {sreg(S_R1)}, {sreg(S_N)}"),
                                           branch("s_cbranch_scc1", f"Llast{q}_{u}")]))
         blocks += step_blocks(f"f{q}", q, "full", f"Linc{q}_{u}")
         tail = [salu(f"s_add_u32 {sreg(S_R1)}, {sreg(S_R1)}, 1")]
-        if q == 3:
-            tail.append(branch("s_branch", f"Lt0_{u}", cond=False))
+        if q == 0:
+            tail.append(branch("s_branch", f"Lt1_{u}", cond=False))
         blocks.append(Block(f"Linc{q}_{u}", tail))
     for q in range(4):
         bl = step_blocks(f"l{q}", q, "last", f"Lepi_{u}")
         bl[0].name = f"Llast{q}_{u}"
         blocks += bl
-    # the shared rescale routine (reached only by branches)
+    # the out-of-line calls, then the shared rescale and recompute routines
+    # (reached only by branches)
+    blocks += COLD
+    COLD.clear()
     blocks.append(Block(f"Lrescale_{u}", rescale_routine()))
+    for par in range(2):
+        for h in range(2):
+            blocks.append(Block(f"Lrecomp{par}{h}_{u}", recompute_routine(par, h)))
     blocks.append(Block(f"Lepi_{u}", epilogue()))
     return blocks
 
@@ -1337,6 +1588,7 @@ def _merge_queues(a, b):
 
 def generate():
     blocks = program()
+    check_returns(blocks)
     waited = insert_waits(blocks)
     for b, w in zip(blocks, waited):
         b.ins = w

@@ -8,7 +8,10 @@ Bars (the target's stated tolerances):
 Configs #1-#4 are checked on every row and head against the oracle (#3 at
 the bench's p_full 0.25; its p_full 0.1 / 0.5 on sampled rows); #5, whose
 dense-prefix oracle takes many minutes, on 1000+ sampled rows weighted to
-the tail.  Size-independent properties must hold bit-exactly at full size.
+the tail.  Size-independent properties hold at full size: the routed call
+against its all-full / all-local runs to rounding (the 256-row kernel's
+rounding can depend on the rows that share a work item), the others bit for
+bit.
 """
 
 import ctypes
@@ -403,19 +406,33 @@ def test_s64k_config_sampled():
 
 
 # ----------------------------------------------------------------------------
-# size-independent properties at full size (bit-exact)
+# size-independent properties at full size
 # ----------------------------------------------------------------------------
 
 def test_routed_equals_rowwise_select_s16k():
-    """Each row depends only on its own route: routed == where(mask, all-full, all-local)."""
+    """Each row depends only on its own route: routed == where(mask,
+    all-full, all-local) up to rounding.  The 256-row kernel takes the
+    exact running max over a work item's first two tiles and checks the
+    exponentials of later ones, so a row's rounding can depend on the rows
+    it shares an item with (where its item's tiles start, whether its wave
+    recomputed a tile): every row agrees within 2e-3 on O (two bf16 ulps
+    at the outputs' magnitude) and 1e-5 on LSE, and no more than 1 % of the
+    rows differ at all."""
     wl = workloads.build("s16k", seed=5, p_full=0.25)
     m = wl["mask"]
     o, lse, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], m, 1024)
     o_f, lse_f, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], torch.ones_like(m), 1024)
     o_l, lse_l, _, _ = _gpu_run(wl["q"], wl["k"], wl["v"], torch.zeros_like(m), 1024)
     md = m.to(DEV)
-    assert torch.equal(o, torch.where(md[..., None, None], o_f, o_l))
-    assert torch.equal(lse, torch.where(md[..., None], lse_f, lse_l))
+    o_sel = torch.where(md[..., None, None], o_f, o_l)
+    l_sel = torch.where(md[..., None], lse_f, lse_l)
+    do = (o.float() - o_sel.float()).abs()
+    dl = (lse - l_sel).abs()
+    rows = int(((do.amax(dim=(-1, -2)) > 0) | (dl.amax(dim=-1) > 0)).sum())
+    print(f"[row select] rows differing {rows} of {m.numel()}, max |dO| {float(do.max()):.3e}, "
+          f"max |dLSE| {float(dl.max()):.3e}", flush=True)
+    assert float(do.max()) <= 2e-3 and float(dl.max()) <= 1e-5
+    assert rows <= m.numel() // 100
 
 
 def _unsplit_run(q, k, v, mask, window, metadata=None):

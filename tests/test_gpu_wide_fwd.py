@@ -9,7 +9,11 @@ shapes of test_gpu_parity (single and partial tiles, W = 1, W >= S,
 G = 1 / 5 / 8, B > 1, Skv != Sq), on packed sequences, on score ranges where
 the running maximum moves often (the rescale path) or keys keep rising along
 the sequence, and on the masked-tile edge cases (windows shorter than a
-64-key tile, rows whose window starts inside a tile).  Bars as in
+64-key tile, rows whose window starts inside a tile), and on keys whose
+scores jump far above everything before them (past an item's first two
+tiles the kernel exponentiates with the running max as it stands and
+checks each half-tile's sums; a failed check, or an exponential beyond the
+fp32 range, has the half recomputed with the exact max).  Bars as in
 test_gpu_parity (O max-abs <= 2e-2, mean-abs <= 2e-3, LSE relative <= 1e-3;
 the NaN / -inf pattern of rows with no key must match the oracle's); the
 two kernels must agree to the same bars, and the 256-row kernel must be
@@ -76,6 +80,32 @@ def test_wide_peaked_and_flat_softmax(monkeypatch, qk_scale, sm_scale):
     o_ref, lse_ref = _oracle(q, k, v, m, 200, sm_scale=sm_scale)
     _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide q,k x{qk_scale} sm_scale {sm_scale}")
     _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow x{qk_scale}")
+
+
+@pytest.mark.parametrize("gamma", [60.0, 400.0])
+def test_wide_score_jumps(monkeypatch, gamma):
+    """Every query shares a component along a unit vector u, and a few keys
+    carry gamma u: their scores jump by about 3 gamma over every key before
+    them, in half 0 and half 1 of tiles 1 to 17 (tile 1 is still taken with
+    the exact max; later ones are checked).  gamma 60 puts P near 2^23 over
+    the running max (the check fails); gamma 400 puts the exponent past 128,
+    so the unchecked exponentials are infinite.  Either way the half is
+    recomputed and the rows match the oracle; rows that never see a jump
+    are untouched by it."""
+    gen = torch.Generator().manual_seed(77)
+    s = 1200
+    q, k, v = workloads.make_qkv(gen, 1, s, s, 8, 2, 128)
+    u = torch.randn(128, generator=gen)
+    u = u / u.norm()
+    qf, kf = q.float() + 3.0 * u, k.float()
+    for pos in (100, 150, 200, 300, 333, 700, 1100):
+        kf[0, pos] += gamma * u
+    q, k = qf.to(torch.bfloat16), kf.to(torch.bfloat16)
+    m = _mask(77, (1, s), 0.4)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 500)
+    o_ref, lse_ref = _oracle(q, k, v, m, 500)
+    _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide score jumps x{gamma}")
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow score jumps x{gamma}")
 
 
 def test_wide_rising_scores(monkeypatch):
