@@ -20,9 +20,10 @@ Issue budget.  One wave per SIMD issues everything in order, and measured
 on gfx950 a wave issues about one instruction per five to six cycles, so
 an MFMA slot (32 cycles for a 32x32x16 bf16 MFMA) holds about five other
 instructions before the matrix core waits.  A step (one 64-key tile: 64
-MFMAs) has about 280 VALU instructions of softmax that cannot be avoided
-(two per exponential, the bf16 packing, the fp32 row sums, the running
-max), so everything else is kept off the path: the K and V^T rings have
+MFMAs) has about 230 VALU instructions of softmax that cannot be avoided
+(two per exponential, the bf16 packing, the fp32 row sums, the checks;
+about 280 where the running max is taken), so everything else is kept off
+the path: the K and V^T rings have
 four slots each and the loop is unrolled four steps, so every LDS operand
 address is a base register plus an immediate offset; the buffer
 descriptors of the global -> LDS copies advance with four scalar
@@ -34,28 +35,45 @@ exponential and never as its first VALU instruction; a 64-key tile has 64
 exponentials and 64 MFMAs, so the exponentials spread over both GEMMs.
 
 Schedule.  The online softmax runs on 32-key halves of each tile (h = 0,
-1; the running max moves at most per half): the scores of half 0 are final
-halfway through S = K Q^T, so its running max can be taken there and its
-exponentials can start as soon as P V of the previous tile does, which runs
-as two 16-MFMA halves.  Each step (tile j) is:
+1; the running max moves at most per half).  The running max is kept as
+n = -m c; a half's max x moves it only when d = x c + n exceeds 8 (P then
+stays below 2^8 without a move), and the rescale exponent e is d or 0.
+Each lane keeps the partial row sum of its own 16 keys of each half; the
+two lanes of a row are added once, at the end.
 
-  -- O, l *= 2^-e(j, 0) when some row's max moved in half 0 of tile j (rare) --
+The pre step (tile 0) and step 0 (tile 1) take that running max exactly,
+so every row whose range starts within an item's first two tiles has a
+finite max.  The steps after them take none: they exponentiate with n as
+it stands and check each half afterwards.  Every lane's sum of its 16 P of
+each row block must be at most 8192 (so every P is, as the online softmax
+needs); a half that fails (the scores jumped, a row met its first key
+late, or 2^x left the fp32 range) branches to an out-of-line routine that
+fetches the tile's K rows from memory, recomputes the half's scores with
+the same MFMAs in the same order, masks them, takes the exact running max
+(whose O, l rescale then follows at the step's rescale point) and redoes
+the exponentials, packing and sums.  A row whose max moved there from a
+finite value had later exponentials taken with the old max: half 0's
+recomputation forces half 1's check to fail, half 1's the next tile's.
+Each step (tile j) is then:
+
   A  (32 MFMAs, S(j+1) half 0 then half 1):  the exponentials of P(j)
-     half 1, packing and row sums of P(j) half 0; then the running max of
-     S(j+1) half 0;
-  B1 (16 MFMAs, P(j) V(j) half 0):  the first 16 exponentials of S(j+1)
-     half 0, packing of P(j) half 1, the running max of S(j+1) half 1;
+     half 1, packing and lane sums of both halves of P(j), the check of
+     half 0 (what is left of half 1 carries on);
+  -- recompute P(j) half 0 when its check failed (rare) --
+  -- O, l *= 2^-e(j, 0) when some row's max moved in half 0 of tile j (rare) --
+  B1 (16 MFMAs, P(j) V(j) half 0):  half 0's sums added to l, the first 16
+     exponentials of S(j+1) half 0, the rest of half 1 and its check;
+  -- recompute P(j) half 1 when its check failed (rare) --
   -- O, l *= 2^-e(j, 1) when some row's max moved in half 1 of tile j (rare) --
-  B2 (16 MFMAs, P(j) V(j) half 1):  the last 16 exponentials of S(j+1)
-     half 0, row sums of P(j) half 1; then the next step's first K and V^T
+  B2 (16 MFMAs, P(j) V(j) half 1):  half 1's sums added to l, the last 16
+     exponentials of S(j+1) half 0; then the next step's first K and V^T
      operands are read (before its barrier).
 
-Work a block cannot fit moves on to the next one (never past a rescale it
-must precede).  The running max is kept as n = -m c; a half's max x moves
-it only when d = x c + n exceeds 8 (P then stays below 2^8 without a
-move), and the rescale exponent e is d or 0.  Each lane keeps the partial
-row sum of its own 16 keys of each half; the two lanes of a row are added
-once, at the end.
+Step 0 instead takes the running max of S(j+1) half 0 in A and of half 1
+in B1, with P(j) half 1 packed in B1 and summed in B2, and no checks.
+Work a block cannot fit moves on to the next one, but never past a check
+the work precedes or a rescale it must precede.  The rare branches go to
+out-of-line blocks after the loop, so the common path falls through.
 
 The output is one inline-asm string for ``swattn_fwd.hip``.  The generator
 places each block's VALU work into its MFMA slots with a list scheduler,
