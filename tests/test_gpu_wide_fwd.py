@@ -108,6 +108,37 @@ def test_wide_score_jumps(monkeypatch, gamma):
     _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow score jumps x{gamma}")
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_wide_random_jumps(monkeypatch, seed):
+    """Randomized checks of the recomputation: a random shape (G = 1, 2, 4
+    or 8, so rows start in late tiles too), window and routing, keys with
+    jumps of random height along a direction the queries share (from a few
+    units to past the fp32 range of 2^x, in either half of random tiles),
+    negative jumps (exponentials that underflow), and a few query rows with
+    outsized norms."""
+    rng = np.random.default_rng(1000 + seed)
+    hkv = int(rng.choice([1, 2, 4]))
+    g = int(rng.choice([1, 2, 4, 8]))
+    s = int(rng.integers(300, 1400))
+    w = int(rng.choice([40, 130, 300, 1000, 4096]))
+    gen = torch.Generator().manual_seed(seed)
+    q, k, v = workloads.make_qkv(gen, 1, s, s, hkv * g, hkv, 128)
+    u = torch.randn(128, generator=gen)
+    u = u / u.norm()
+    qf, kf = q.float() + 3.0 * u, k.float()
+    for pos in rng.choice(s, size=int(rng.integers(3, 9)), replace=False):
+        kf[0, int(pos), int(rng.integers(hkv))] += float(rng.choice([-200.0, 8.0, 25.0, 60.0, 400.0])) * u
+    for row in rng.choice(s, size=4, replace=False):
+        qf[0, int(row)] *= 20.0
+    q, k = qf.to(torch.bfloat16), kf.to(torch.bfloat16)
+    m = _mask(seed, (1, s), float(rng.choice([0.0, 0.3, 1.0])))
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, w)
+    o_ref, lse_ref = _oracle(q, k, v, m, w)
+    tag = f"wide random jumps seed {seed}: s{s} g{g} hkv{hkv} w{w}"
+    _assert_close(ow, lw, o_ref, lse_ref, tag=tag)
+    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=tag + " vs narrow")
+
+
 def test_wide_rising_scores(monkeypatch):
     """Keys whose scores against every query rise along the sequence (each
     key a growing multiple of one direction shared with the queries), so
