@@ -702,7 +702,7 @@ def half_regs(s, h):
 
 
 # the temporaries of mask() and the row sums a recomputation also writes
-CHECK_TEMPS = ({f"v{V_L}", f"v{V_L + 1}", f"v{V_CHK}"} | regs("v", V_LO, 2) | regs("v", V_MK, 4) |
+CHECK_TEMPS = ({f"v{V_L}", f"v{V_L + 1}", f"v{V_CHK}", "vcc"} | regs("v", V_LO, 2) | regs("v", V_MK, 4) |
                regs("s", S_PAIRS[0], 8) | regs("s", S_T0, 2))
 
 
@@ -895,8 +895,10 @@ def _cold_call(tag, skip, target, prep=()):
 
 
 def check_returns(blocks):
-    """Every return address is formed as pc - (pc - skip): the skip label
-    must come before the call's pc label in the layout."""
+    """A return address formed as pc - (pc - skip) needs the skip label
+    before the call's pc label in the layout, one formed as pc + (ret - pc)
+    (the 32-bit difference with a carry into the high word) the return
+    label after it."""
     pos = {}
     n = 0
     for b in blocks:
@@ -910,7 +912,9 @@ def check_returns(blocks):
             if ins.text.startswith(f"s_sub_u32 {sreg(S_RET)}, {sreg(S_RET)}, "):
                 pc, skip = ins.text.split(", ")[-1].split("-")
                 assert pos[skip] < pos[pc], f"return label {skip} after its call"
-            assert not ins.text.startswith(f"s_add_u32 {sreg(S_RET)},"), "return address formed by an add"
+            if ins.text.startswith(f"s_add_u32 {sreg(S_RET)}, {sreg(S_RET)}, "):
+                ret, pc = ins.text.split(", ")[-1].split("-")
+                assert pos[ret] > pos[pc], f"return label {ret} before its call"
 
 
 def call_rescale(tag, par, h):
@@ -936,34 +940,68 @@ def call_rescale(tag, par, h):
 
 
 def call_recompute(tag, par, h, head):
-    """Blocks that end `head` with the check of half h of tile j (parity
-    par): every lane's 16-key sums of its two row blocks (left by
-    sums_tree) at most the threshold, and no recomputation forced;
-    else (rarely, out of line) drain the LDS reads and branch to the shared
-    routine that recomputes the half's scores with the exact running max."""
+    """Blocks that end `head` with the test that check_items left: nothing
+    to do unless half h of tile j (parity par) failed its check or its
+    rescale flag is set.  Then, out of line: the recomputation if the check
+    failed (its routine returns into the out-of-line blocks), and the O, l
+    rescale if the flag is set (then cleared), with the LDS reads drained
+    before each branch to a shared routine; back to the step after."""
     u = "%="
     skip = f"L{tag}_x_{u}"
     pr = S_T0
-    call = _cold_call(tag, skip, f"Lrecomp{par}{h}_{u}")
-    chk = [salu(f"s_cmp_lg_u64 {sreg(pr, 2)}, 0", {f"s{pr}", f"s{pr + 1}"}), branch("s_cbranch_scc1", call)]
+    flag = S_FLAG + 4 * par + 2 * h
+    al = V_AL + 2 * par + h
+    cold, resc, back = f"L{tag}_o_{u}", f"L{tag}_r_{u}", f"L{tag}_b_{u}"
+    pc0, pc1 = f"L{tag}_pc_{u}", f"L{tag}_pd_{u}"
+    COLD.extend([
+        Block(cold, [salu("s_cmp_lg_u64 vcc, 0", {"vcc"}), branch("s_cbranch_scc0", resc)]),
+        Block(f"L{tag}_c_{u}", [
+            waitcnt(lgkm=0),
+            Ins(f"s_getpc_b64 {sreg(S_RET, 2)}", "salu", set(), {f"s{S_RET}", f"s{S_RET + 1}"}),
+            label(pc0),
+            salu(f"s_add_u32 {sreg(S_RET)}, {sreg(S_RET)}, {resc}-{pc0}"),
+            salu(f"s_addc_u32 {sreg(S_RET + 1)}, {sreg(S_RET + 1)}, 0"),
+            Ins(f"s_branch Lrecomp{par}{h}_{u}", "call", branch=f"Lrecomp{par}{h}_{u}", cond=False)]),
+        Block(resc, [salu(f"s_cmp_lg_u64 {sreg(flag, 2)}, 0"),
+                     salu(f"s_mov_b64 {sreg(flag, 2)}, 0", wr={f"s{flag}", f"s{flag + 1}"}),
+                     branch("s_cbranch_scc0", back)], ret_point=True),
+        Block(f"L{tag}_s_{u}", [
+            valu(f"v_mov_b32 {vreg(V_RA)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA}"}),
+            valu(f"v_mov_b32 {vreg(V_RA + 1)}, {vreg(al)}", {f"v{al}"}, {f"v{V_RA + 1}"}),
+            Ins(f"v_permlane32_swap_b32 {vreg(V_RA)}, {vreg(V_RA + 1)}", "perm", {f"v{V_RA}", f"v{V_RA + 1}"},
+                {f"v{V_RA}", f"v{V_RA + 1}"}),
+            waitcnt(lgkm=0),
+            Ins(f"s_getpc_b64 {sreg(S_RET, 2)}", "salu", set(), {f"s{S_RET}", f"s{S_RET + 1}"}),
+            label(pc1),
+            salu(f"s_sub_u32 {sreg(S_RET)}, {sreg(S_RET)}, {pc1}-{skip}"),
+            salu(f"s_subb_u32 {sreg(S_RET + 1)}, {sreg(S_RET + 1)}, 0"),
+            Ins(f"s_branch Lrescale_{u}", "call", branch=f"Lrescale_{u}", cond=False)]),
+        Block(back, [branch("s_branch", skip, cond=False)]),
+    ])
+    chk = [salu(f"s_cmp_lg_u64 {sreg(pr, 2)}, 0", {f"s{pr}", f"s{pr + 1}"}), branch("s_cbranch_scc1", cold)]
     return [Block(f"L{tag}_k_{u}", head + chk), Block(skip, [], ret_point=True)]
 
 
 def check_items(par, h):
     """The test of half h of tile j (parity par) that call_recompute
-    branches on, as ordinary work for the scheduler: s[S_T0:S_T0+1] = lanes
-    whose 16-key sum of either row block (left by sums_tree) exceeds the
-    threshold, or every lane when a recomputation is forced."""
+    branches on, as ordinary work for the scheduler: vcc = lanes whose
+    16-key sum of either row block (left by sums_tree) exceeds the
+    threshold, or every lane when a recomputation is forced; s[S_T0:S_T0+1]
+    = vcc or the half's rescale flag (steps without a running max set that
+    flag only by recomputing, after this test, or in step 0 for tile 1,
+    before it)."""
     s = S_V[par]
     pr = S_T0
     force = S_FORCE if h == 0 else S_FORCE1
+    flag = S_FLAG + 4 * par + 2 * h
     return [valu(f"v_max_f32 {vreg(V_CHK)}, {vreg(s + 16 * h)}, {vreg(s + 32 + 16 * h)}",
                  {f"v{s + 16 * h}", f"v{s + 32 + 16 * h}"}, {f"v{V_CHK}"}),
-            valu(f"v_cmp_lt_f32_e64 {sreg(pr, 2)}, {vreg(V_THR)}, {vreg(V_CHK)}", {f"v{V_THR}", f"v{V_CHK}"},
-                 {f"s{pr}", f"s{pr + 1}"}),
+            valu(f"v_cmp_lt_f32_e64 vcc, {vreg(V_THR)}, {vreg(V_CHK)}", {f"v{V_THR}", f"v{V_CHK}"}, {"vcc"}),
             # mask_rd: keeps the scalar read three instructions after the compare
-            Ins(f"s_or_b64 {sreg(pr, 2)}, {sreg(pr, 2)}, {sreg(force, 2)}", "salu",
-                {f"s{force}", f"s{force + 1}"}, {f"s{pr}", f"s{pr + 1}"}, mask_rd={f"s{pr}", f"s{pr + 1}"})]
+            Ins(f"s_or_b64 vcc, vcc, {sreg(force, 2)}", "salu", {f"s{force}", f"s{force + 1}"}, {"vcc"},
+                mask_rd={"vcc"}),
+            salu(f"s_or_b64 {sreg(pr, 2)}, vcc, {sreg(flag, 2)}", {"vcc", f"s{flag}", f"s{flag + 1}"},
+                 {f"s{pr}", f"s{pr + 1}"})]
 
 
 def recompute_routine(par, h):
@@ -1035,10 +1073,8 @@ def opt_tail(tag, q, kind, masked):
     par = q % 2
     a, left = block_a(q, kind, masked, opt=True)
     bl = call_recompute(f"{tag}k0", par, 0, a)
-    bl += call_rescale(f"{tag}r0", par, 0)
     b1, left = block_b1(q, kind, masked, left, opt=True)
     bl += call_recompute(f"{tag}k1", par, 1, b1)
-    bl += call_rescale(f"{tag}r1", par, 1)
     bl.append(Block(f"L{tag}_b2_{u}", block_b2(q, kind, left, opt=True)))
     return bl
 
