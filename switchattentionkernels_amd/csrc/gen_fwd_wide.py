@@ -53,27 +53,36 @@ the same MFMAs in the same order, masks them, takes the exact running max
 (whose O, l rescale then follows at the step's rescale point) and redoes
 the exponentials, packing and sums.  A row whose max moved there from a
 finite value had later exponentials taken with the old max: half 0's
-recomputation forces half 1's check to fail, half 1's the next tile's.
-Each step (tile j) is then:
+recomputation forces half 1's check to fail (and the next tile's half 0),
+half 1's the next tile's.
 
-  A  (32 MFMAs, S(j+1) half 0 then half 1):  the exponentials of P(j)
-     half 1, packing and lane sums of both halves of P(j), the check of
-     half 0 (what is left of half 1 carries on);
-  -- recompute P(j) half 0 when its check failed (rare) --
-  -- O, l *= 2^-e(j, 0) when some row's max moved in half 0 of tile j (rare) --
-  B1 (16 MFMAs, P(j) V(j) half 0):  half 0's sums added to l, the first 16
+A step (tile j) starts with P(j) half 0 exponentiated, packed and its
+sums' first level formed, and the first 16 exponentials of P(j) half 1
+taken.  It is then:
+
+  A  (32 MFMAs, S(j+1) half 0 then half 1):  the last 16 exponentials of
+     P(j) half 1, the rest of half 0's lane sums and its check; once S(j+1)
+     half 0 is final, its first 16 exponentials; then packing and lane sums
+     of P(j) half 1 (what is left of them carries on);
+  -- recompute P(j) half 0 when its check failed, O, l *= 2^-e(j, 0) when
+     some row's max moved in half 0 of tile j (rare, out of line) --
+  B1 (16 MFMAs, P(j) V(j) half 0):  half 0's sums added to l, the last 16
      exponentials of S(j+1) half 0, the rest of half 1 and its check;
-  -- recompute P(j) half 1 when its check failed (rare) --
-  -- O, l *= 2^-e(j, 1) when some row's max moved in half 1 of tile j (rare) --
-  B2 (16 MFMAs, P(j) V(j) half 1):  half 1's sums added to l, the last 16
-     exponentials of S(j+1) half 0; then the next step's first K and V^T
-     operands are read (before its barrier).
+  -- the same for half 1 of tile j --
+  B2 (16 MFMAs, P(j) V(j) half 1):  half 1's sums added to l, the first 16
+     exponentials of S(j+1) half 1, packing and first sum level of S(j+1)
+     half 0; then the next step's first K and V^T operands are read
+     (before its barrier).
 
-Step 0 instead takes the running max of S(j+1) half 0 in A and of half 1
-in B1, with P(j) half 1 packed in B1 and summed in B2, and no checks.
-Work a block cannot fit moves on to the next one, but never past a check
-the work precedes or a rescale it must precede.  The rare branches go to
-out-of-line blocks after the loop, so the common path falls through.
+Each half's packing and sums thus get about 32 MFMA slots before its
+check.  The first exponentials of S(j+1) half 0 are taken before P(j)
+half 0's check, so a recomputation of half 0 that moves a row's max from
+a finite value forces the next tile's half-0 check too.  Step 0 takes the
+running max of S(j+1) half 0 in A (before its exponentials) and of half 1
+in B1, has no checks, and applies O, l *= 2^-e at the step's start and
+between B1 and B2.  Work a block cannot fit moves on to the next one, but
+never past a check the work precedes or a rescale it must precede, nor
+past a step's end.
 
 The output is one inline-asm string for ``swattn_fwd.hip``.  The generator
 places each block's VALU work into its MFMA slots with a list scheduler,
@@ -368,9 +377,15 @@ def sums(s, h):
 def sums_tree(s, h):
     """This lane's sum of its 16 fp32 P of half h for each row block, in
     place (after the packing), left in the half's first register."""
+    return tree_levels(s, h, 16, 1)
+
+
+def tree_levels(s, h, top, bottom):
+    """The levels of sums_tree from `top` partial sums per row block down
+    to `bottom` (16 -> 8 is the first level)."""
     out = []
-    width = 16
-    while width > 1:
+    width = top
+    while width > bottom:
         hw = width // 2
         for i in range(hw):
             for rb in range(2):
@@ -707,22 +722,26 @@ CHECK_TEMPS = ({f"v{V_L}", f"v{V_L + 1}", f"v{V_CHK}", "vcc"} | regs("v", V_LO, 
 
 
 def block_a(q, kind, masked, opt=False):
-    """S(j+1) = K(j+1) Q^T in 32 MFMAs (half 0, then half 1) while P(j)
-    half 1 is exponentiated, P(j) half 0 packed and summed, and S(j+1)
-    half 0's running max taken.  kind 'pre' (tile 0's S only), 'full',
-    'last' (no S(j+1)).  With opt no running max is taken, P(j) half 0's
-    lane sums stay for its check, and P(j) half 1 is also packed and its
-    lane sums formed; what is left over of that half 1 work is carried on
-    (the rest is issued before the check).  Returns (instructions,
-    leftover VALU)."""
+    """S(j+1) = K(j+1) Q^T in 32 MFMAs (half 0, then half 1).  A step
+    starts with P(j) half 0 exponentiated, packed and its sums' first level
+    formed, and the first 16 exponentials of P(j) half 1 taken (by the
+    previous step's B2).  A takes the last 16 exponentials of P(j) half 1
+    and the rest of half 0's sums (and, with opt, half 0's check); once
+    S(j+1) half 0 is final, its mask, (without opt) its running max, and
+    its first 16 exponentials; then P(j) half 1 is packed and its sums
+    formed, work that may carry on into B1 (with opt, what is left of half
+    0 is issued before the check instead).  kind 'pre' (tile 0's S and the
+    work a step starts with), 'full', 'last' (no S(j+1)).  Returns
+    (instructions, leftover VALU)."""
     par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
     pn = 1 - par           # parity of tile j + 1
     ks = (q + 1) % 4
+    nh = 1 if opt else None
     out = []
     vl = []
     if kind != "pre":
-        vl += exps(scur, 1, 0, 32) + packs(scur, 0) + (sums_tree(scur, 0) if opt else sums(scur, 0))
+        vl += exps(scur, 1, 16, 32) + tree_levels(scur, 0, 8, 1)
         if opt:
             vl += check_items(par, 0)
     if kind != "last":
@@ -732,7 +751,8 @@ def block_a(q, kind, masked, opt=False):
             vl += mask(snxt, 0)
         if not opt:
             vl += running_max(snxt, 0, pn)
-    if opt and kind != "pre":
+        vl += exps(snxt, 0, 0, 16 if kind != "pre" else 32, nh)
+    if kind != "pre":
         vl += packs(scur, 1) + sums_tree(scur, 1)
     if kind == "last":
         out += [v_read(*x, q) for x in V_SEQ[N_PRE_V:V_SETS - 1]]
@@ -769,29 +789,30 @@ def block_a(q, kind, masked, opt=False):
 
 
 def block_b1(q, kind, masked, carried, opt=False):
-    """P(j) V(j) for half 0 (16 MFMAs) while S(j+1) half 0 is exponentiated
-    (first 16 of 32), P(j) half 1 packed and S(j+1) half 1's running max
-    taken.  With opt: P(j) half 0's lane sums are added to l first, S(j+1)
-    half 0 is exponentiated with the running max as it stands, no max is
-    taken, and what is left over of P(j) half 1 or the masks is issued
-    before the half-1 check (the exponentials are carried on).  Returns
+    """P(j) V(j) for half 0 (16 MFMAs) while P(j) half 0's sums are added
+    to l, S(j+1) half 0 takes its last 16 exponentials, S(j+1) half 1 is
+    masked and (without opt) given its running max, and P(j) half 1's
+    packing and sums carried from A finish (with opt, with its check; what
+    is left of half 1 is then issued before the check, the exponentials
+    carry on).  kind 'pre': the V^T copies of the pre step only.  Returns
     (instructions, leftover VALU)."""
     par = q % 2
     snxt, scur = S_V[1 - par], S_V[par]
     pn = 1 - par
+    nh = 1 if opt else None
     vl = list(carried)
     nc = len(vl)
-    if opt and kind != "pre":
-        vl += check_items(par, 1) + sums_add(scur, 0)
-    if kind != "last":
-        vl += exps(snxt, 0, 0, 16, nh=1 if opt else None)
-    if kind != "pre" and not opt:
-        vl += packs(scur, 1)
+    if kind != "pre":
+        vl += sums_add(scur, 0)
+    if kind == "full":
+        vl += exps(snxt, 0, 16, 32, nh)
     if kind != "last":
         if masked:
             vl += mask(snxt, 1)
         if not opt:
             vl += running_max(snxt, 1, pn)
+    if opt and kind != "pre":
+        vl += check_items(par, 1)
     dmas = [dma("v", i, (q + 3) % 4) for i in range(4)] if kind != "last" else []
     if kind == "pre":
         o, _ = schedule([], vl)
@@ -814,29 +835,27 @@ def block_b1(q, kind, masked, carried, opt=False):
                 r += desc_advance("v")
         return r
     o, left = schedule(mf, vl, side, carry=True, n_carried=nc, lead_cap=0)
-    if opt:
-        must, left = split_left(left, half_regs(scur, 1) | CHECK_TEMPS)
-        o += must
-    for x in left:
-        assert f"v{V_L}" not in x.wr, "the half-0 row sums must be added before the half-1 rescale"
+    must, left = split_left(left, (half_regs(scur, 1) | CHECK_TEMPS) if opt else {f"v{V_L}", f"v{V_L + 1}"})
+    o += must
     return o, left
 
 
 def block_b2(q, kind, carried, opt=False):
-    """P(j) V(j) for half 1 (16 MFMAs) while S(j+1) half 0's last 16
-    exponentials run and P(j) half 1 is summed (with opt: its lane sums,
-    formed before the check, added to l); then the next step's first K(j+2)
-    and V^T(j+1) operands are read."""
+    """P(j) V(j) for half 1 (16 MFMAs) while P(j) half 1's sums are added
+    to l and S(j+1) half 1 takes its first 16 exponentials, S(j+1) half 0
+    is packed and its sums' first level formed (the state the next step
+    starts with); then the next step's first K(j+2) and V^T(j+1) operands
+    are read.  kind 'pre': S(0) half 1's first 16 exponentials, S(0) half
+    0's packing and first level, then the pre step's own barrier."""
     par = q % 2
     scur, snxt = S_V[par], S_V[1 - par]
+    nh = 1 if opt else None
     vl = list(carried)
     nc = len(vl)
-    if opt and kind != "pre":
+    if kind != "pre":
         vl += sums_add(scur, 1)
     if kind != "last":
-        vl += exps(snxt, 0, 16, 32, nh=1 if opt else None)
-    if kind != "pre" and not opt:
-        vl += sums(scur, 1)
+        vl += exps(snxt, 1, 0, 16, nh) + packs(snxt, 0) + tree_levels(snxt, 0, 16, 8)
     mf = []
     if kind != "pre":
         for s2 in (2, 3):
@@ -1055,12 +1074,19 @@ def recompute_routine(par, h):
     o, _ = schedule([], vl)
     out += o
     flag = S_FLAG + 4 * par + 2 * h
-    fset, fclr = (S_FORCE1, S_FORCE) if h == 0 else (S_FORCE, S_FORCE1)
-    out += [salu(f"s_mov_b64 {sreg(fset, 2)}, {sreg(flag, 2)}", {f"s{flag}", f"s{flag + 1}"},
-                 {f"s{fset}", f"s{fset + 1}"}),
-            salu(f"s_mov_b64 {sreg(fclr, 2)}, 0", set(), {f"s{fclr}", f"s{fclr + 1}"}),
-            Ins("s_nop 15", "nop"),
-            Ins(f"s_setpc_b64 {sreg(S_RET, 2)}", "ret")]
+    if h == 0:
+        # half 1 of this tile and the first exponentials of the next tile's
+        # half 0 were taken with the old max
+        out += [salu(f"s_mov_b64 {sreg(S_FORCE1, 2)}, {sreg(flag, 2)}", {f"s{flag}", f"s{flag + 1}"},
+                     {f"s{S_FORCE1}", f"s{S_FORCE1 + 1}"}),
+                salu(f"s_mov_b64 {sreg(S_FORCE, 2)}, {sreg(flag, 2)}", {f"s{flag}", f"s{flag + 1}"},
+                     {f"s{S_FORCE}", f"s{S_FORCE + 1}"})]
+    else:
+        out += [salu(f"s_or_b64 {sreg(S_FORCE, 2)}, {sreg(S_FORCE, 2)}, {sreg(flag, 2)}",
+                     {f"s{flag}", f"s{flag + 1}", f"s{S_FORCE}", f"s{S_FORCE + 1}"},
+                     {f"s{S_FORCE}", f"s{S_FORCE + 1}"}),
+                salu(f"s_mov_b64 {sreg(S_FORCE1, 2)}, 0", set(), {f"s{S_FORCE1}", f"s{S_FORCE1 + 1}"})]
+    out += [Ins("s_nop 15", "nop"), Ins(f"s_setpc_b64 {sreg(S_RET, 2)}", "ret")]
     return out
 
 
