@@ -4,7 +4,10 @@ against the 128-row kernel.
 
 swattn_prefill_fwd picks the 256-row kernel by itself only for large grids
 (1024 work items or more), which the config-sized tests cover; here
-SWATTN_FWD_KERNEL=wide / narrow forces one kernel or the other on the small
+SWATTN_FWD_KERNEL=wide / narrow forces one kernel or the other, through the
+C ABI with the plain workspace (which never takes the key-range split: with
+the public API's split workspace, long full rows on these small grids
+would run the 128-row kernel whatever the variable says), on the small
 shapes of test_gpu_parity (single and partial tiles, W = 1, W >= S,
 G = 1 / 5 / 8, B > 1, Skv != Sq), on packed sequences, on score ranges where
 the running maximum moves often (the rescale path) or keys keep rising along
@@ -15,9 +18,9 @@ tiles the kernel exponentiates with the running max as it stands and
 checks each half-tile's sums; a failed check, or an exponential beyond the
 fp32 range, has the half recomputed with the exact max).  Bars as in
 test_gpu_parity (O max-abs <= 2e-2, mean-abs <= 2e-3, LSE relative <= 1e-3;
-the NaN / -inf pattern of rows with no key must match the oracle's); the
-two kernels must agree to the same bars, and the 256-row kernel must be
-deterministic.
+the NaN / -inf pattern of rows with no key must match the oracle's), for
+both kernels; between them O must agree within two bf16 ulps plus 1e-2
+and LSE to 1e-3, and the 256-row kernel must be deterministic.
 """
 
 import numpy as np
@@ -26,20 +29,75 @@ import torch
 
 import oracle
 from oracle import routing as R
-from switchattentionkernels_amd import (build_switch_query_indices,
+from switchattentionkernels_amd import (build_switch_attention_metadata, build_switch_query_indices,
                                         switch_gqa_prefill_varlen_forward, workloads)
 
-from test_gpu_parity import SMALL, _assert_close, _gpu_run, _mask, _oracle, _qkv
+from test_gpu_parity import SMALL, _assert_close, _mask, _oracle, _qkv
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _both(monkeypatch, q, k, v, m, w, **kw):
+def _plain_run(q, k, v, mask, window, metadata=None, sm_scale=None):
+    """swattn_prefill_fwd through the C ABI with the plain workspace
+    (swattn_prefill_workspace_bytes).  The public API passes the larger
+    split workspace, and where the key-range split is planned (long full
+    rows on small grids) it runs the 128-row kernel whatever
+    SWATTN_FWD_KERNEL says; with the plain workspace the forced kernel
+    runs."""
+    import ctypes
+    from switchattentionkernels_amd import _lib
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, local = build_switch_query_indices(mask.to(DEV))
+    b, s, hq, _ = q.shape
+    skv, hkv = k.shape[1], k.shape[2]
+    L = _lib.lib()
+    ws_bytes = L.swattn_prefill_workspace_bytes(b, skv, hkv, 128)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=DEV)
+    md = metadata
+    scale = (128 ** -0.5 if sm_scale is None else sm_scale) * oracle.LOG2E
+    st = L.swattn_prefill_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), full.data_ptr(),
+                              full.numel(), local.data_ptr(), local.numel(),
+                              _lib.ptr(md.full_starts) if md is not None else None,
+                              _lib.ptr(md.local_starts) if md is not None else None,
+                              _lib.ptr(md.causal_ends) if md is not None else None,
+                              out.data_ptr(), lse.data_ptr(), b, s, skv, hq, hkv, 128, window,
+                              ctypes.c_float(scale), ws.data_ptr(), ws_bytes, _lib.stream_handle(q.device))
+    assert st == 0, L.swattn_last_error()
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def _kernels_agree(ow, lw, on, ln, tag):
+    """The two kernels' outputs for the same rows: the same NaN / -inf
+    pattern, O within two bf16 ulps of the larger magnitude plus 1e-2 (half
+    the oracle bar; the rounding of P moves outputs by a share of |V|, not of
+    |O|), LSE within 1e-3 relative.  Each kernel is held to the oracle bars
+    separately; between two bf16 results the oracle's absolute bar alone
+    would be too tight for large outputs (nearly one-hot rows give |O| up
+    to about 5, where one ulp is 0.03)."""
+    a, b = ow.float().cpu(), on.float().cpu()
+    assert torch.equal(torch.isnan(a), torch.isnan(b)), f"{tag}: NaN patterns differ"
+    assert torch.equal(torch.isneginf(lw.cpu()), torch.isneginf(ln.cpu())), f"{tag}: -inf LSE patterns differ"
+    fin = ~torch.isnan(a)
+    d, mag = (a - b).abs()[fin], torch.maximum(a.abs(), b.abs())[fin]
+    worst = float((d - mag * 2 ** -6).max()) if d.numel() else 0.0
+    la, lb = lw.cpu(), ln.cpu()
+    lf = torch.isfinite(la)
+    lrel = float(((la - lb).abs()[lf] / la.abs()[lf].clamp(min=1.0)).max()) if lf.any() else 0.0
+    print(f"{tag}: O max {float(d.max()) if d.numel() else 0:.3e} (excess over 2 ulps {worst:.3e}), "
+          f"LSE rel {lrel:.3e}", flush=True)
+    assert worst <= 1e-2, f"{tag}: O differs by more than two bf16 ulps plus 1e-2"
+    assert lrel <= 1e-3, f"{tag}: LSE rel {lrel}"
+
+
+def _both(monkeypatch, q, k, v, m, w, metadata=None, sm_scale=None):
     monkeypatch.setenv("SWATTN_FWD_KERNEL", "wide")
-    ow, lw, _, _ = _gpu_run(q, k, v, m, w, **kw)
+    ow, lw = _plain_run(q, k, v, m, w, metadata=metadata, sm_scale=sm_scale)
     monkeypatch.setenv("SWATTN_FWD_KERNEL", "narrow")
-    on, ln, _, _ = _gpu_run(q, k, v, m, w, **kw)
+    on, ln = _plain_run(q, k, v, m, w, metadata=metadata, sm_scale=sm_scale)
     monkeypatch.delenv("SWATTN_FWD_KERNEL")
     return ow, lw, on, ln
 
@@ -52,7 +110,8 @@ def test_wide_small(monkeypatch, b, s, hq, hkv, w, p, skv):
     o_ref, lse_ref = _oracle(q, k, v, m, w)
     tag = f"b{b} s{s} {hq}/{hkv} w{w} p{p} skv{skv}"
     _assert_close(ow, lw, o_ref, lse_ref, tag="wide " + tag)
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow " + tag)
+    _assert_close(on, ln, o_ref, lse_ref, tag="narrow " + tag)
+    _kernels_agree(ow, lw, on, ln, tag="wide vs narrow " + tag)
 
 
 @pytest.mark.parametrize("w", [1, 7, 40, 64, 65, 130])
@@ -65,7 +124,8 @@ def test_wide_masked_tiles(monkeypatch, w):
     ow, lw, on, ln = _both(monkeypatch, q, k, v, m, w)
     o_ref, lse_ref = _oracle(q, k, v, m, w)
     _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide w{w}")
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow w{w}")
+    _assert_close(on, ln, o_ref, lse_ref, tag=f"narrow w{w}")
+    _kernels_agree(ow, lw, on, ln, tag=f"wide vs narrow w{w}")
 
 
 @pytest.mark.parametrize("qk_scale,sm_scale", [(4.0, None), (1.0, 1.0), (0.05, None), (8.0, 1.0)])
@@ -79,7 +139,8 @@ def test_wide_peaked_and_flat_softmax(monkeypatch, qk_scale, sm_scale):
     ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 200, sm_scale=sm_scale)
     o_ref, lse_ref = _oracle(q, k, v, m, 200, sm_scale=sm_scale)
     _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide q,k x{qk_scale} sm_scale {sm_scale}")
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow x{qk_scale}")
+    _assert_close(on, ln, o_ref, lse_ref, tag=f"narrow x{qk_scale}")
+    _kernels_agree(ow, lw, on, ln, tag=f"wide vs narrow x{qk_scale}")
 
 
 @pytest.mark.parametrize("gamma", [60.0, 400.0])
@@ -105,7 +166,8 @@ def test_wide_score_jumps(monkeypatch, gamma):
     ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 500)
     o_ref, lse_ref = _oracle(q, k, v, m, 500)
     _assert_close(ow, lw, o_ref, lse_ref, tag=f"wide score jumps x{gamma}")
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=f"wide vs narrow score jumps x{gamma}")
+    _assert_close(on, ln, o_ref, lse_ref, tag=f"narrow score jumps x{gamma}")
+    _kernels_agree(ow, lw, on, ln, tag=f"wide vs narrow score jumps x{gamma}")
 
 
 @pytest.mark.parametrize("seed", range(12))
@@ -136,7 +198,8 @@ def test_wide_random_jumps(monkeypatch, seed):
     o_ref, lse_ref = _oracle(q, k, v, m, w)
     tag = f"wide random jumps seed {seed}: s{s} g{g} hkv{hkv} w{w}"
     _assert_close(ow, lw, o_ref, lse_ref, tag=tag)
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag=tag + " vs narrow")
+    _assert_close(on, ln, o_ref, lse_ref, tag="narrow " + tag)
+    _kernels_agree(ow, lw, on, ln, tag=tag + " vs narrow")
 
 
 def test_wide_rising_scores(monkeypatch):
@@ -157,7 +220,8 @@ def test_wide_rising_scores(monkeypatch):
     ow, lw, on, ln = _both(monkeypatch, q, k, v, m, 300)
     o_ref, lse_ref = _oracle(q, k, v, m, 300)
     _assert_close(ow, lw, o_ref, lse_ref, tag="wide rising scores")
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow rising scores")
+    _assert_close(on, ln, o_ref, lse_ref, tag="narrow rising scores")
+    _kernels_agree(ow, lw, on, ln, tag="wide vs narrow rising scores")
 
 
 def test_wide_varlen(monkeypatch):
@@ -168,21 +232,18 @@ def test_wide_varlen(monkeypatch):
     gen = torch.Generator().manual_seed(8)
     q, k, v = workloads.make_qkv(gen, 1, t, t, hq, hkv, 128)
     mask = torch.rand((1, t), generator=gen) < 0.4
+    meta = build_switch_attention_metadata(t, t, device=DEV, window_size=w, cu_seqlens=cu)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, mask, w, metadata=meta)
     full, local = build_switch_query_indices(mask.to(DEV))
-    outs = {}
-    for kind in ("wide", "narrow"):
-        monkeypatch.setenv("SWATTN_FWD_KERNEL", kind)
-        outs[kind] = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local,
-                                                       cu, window_size=w)
-        torch.cuda.synchronize()
-    monkeypatch.delenv("SWATTN_FWD_KERNEL")
+    api_o, api_l = switch_gqa_prefill_varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), full, local, cu,
+                                                     window_size=w)
     md = R.varlen_metadata(cu, cu, w)
     f_o, l_o = R.compact(mask.numpy())
     o_ref, lse_ref = oracle.routed_attention(q, k, v, f_o, l_o, metadata=md)
-    ow, lw = outs["wide"]
-    on, ln = outs["narrow"]
+    _assert_close(api_o, api_l, o_ref, lse_ref, tag="varlen entry point")
     _assert_close(ow, lw, o_ref, lse_ref, tag="wide varlen")
-    _assert_close(ow, lw, on.float().cpu(), ln.cpu(), tag="wide vs narrow varlen")
+    _assert_close(on, ln, o_ref, lse_ref, tag="narrow varlen")
+    _kernels_agree(ow, lw, on, ln, tag="wide vs narrow varlen")
 
 
 def test_wide_deterministic_and_every_row_written(monkeypatch):
