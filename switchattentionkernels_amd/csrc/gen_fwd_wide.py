@@ -367,16 +367,11 @@ def swap_combine(x, t, op):
             valu(f"{op} {vreg(x)}, {vreg(x)}, {vreg(t)}", {f"v{x}", f"v{t}"}, {f"v{x}"})]
 
 
-def sums(s, h):
-    """Row sums of the fp32 P of half h (in place, after its packing), added
-    to this lane's partial l (the two lanes of a row keep partial sums of
-    their own keys; they are combined once, at the end)."""
-    return sums_tree(s, h) + sums_add(s, h)
-
-
 def sums_tree(s, h):
     """This lane's sum of its 16 fp32 P of half h for each row block, in
-    place (after the packing), left in the half's first register."""
+    place (after the packing), left in the half's first register (the two
+    lanes of a row keep partial sums of their own keys, combined once, at
+    the end)."""
     return tree_levels(s, h, 16, 1)
 
 
