@@ -278,3 +278,21 @@ def test_wide_deterministic_and_every_row_written(monkeypatch):
     rows = np.arange(0, b * s, 13)
     o_ref, lse_ref = _oracle(q.cpu(), k.cpu(), v.cpu(), m.cpu(), w, rows=rows)
     _assert_close(o1, l1, o_ref, lse_ref, rows=rows, tag="wide b2 s1500 sampled")
+
+
+@pytest.mark.parametrize("b,s,hq,hkv,w,p", [(2, 2048, 32, 8, 512, 0.1), (1, 4096, 40, 8, 4096, 0.1),
+                                            (1, 6144, 32, 8, 1024, 0.25)])
+def test_wide_sparse_full_list_mid_grid(monkeypatch, b, s, hq, hkv, w, p):
+    """Grids of 520-776 work items with a sparse full list, where a 256-row
+    item's rows spread over hundreds of positions (G = 4 and 5) and its key
+    range is the union of theirs: both kernels against the oracle on sampled
+    rows and against each other on every row."""
+    q, k, v = _qkv(s + hq + w, b, s, hq, hkv)
+    m = _mask(s + w, (b, s), p)
+    ow, lw, on, ln = _both(monkeypatch, q, k, v, m, w)
+    tag = f"b{b} s{s} {hq}/{hkv} w{w} p{p}"
+    rows = np.arange(0, b * s, 17)
+    o_ref, lse_ref = _oracle(q, k, v, m, w, rows=rows)
+    _assert_close(ow, lw, o_ref, lse_ref, rows=rows, tag="wide " + tag)
+    _assert_close(on, ln, o_ref, lse_ref, rows=rows, tag="narrow " + tag)
+    _kernels_agree(ow, lw, on, ln, tag="wide vs narrow " + tag)
